@@ -1,0 +1,182 @@
+/*
+ * tileops_hip.h -- C ABI of the MI355X (gfx950) TileOPs forward-operator
+ * library, libtileops_hip.so.
+ *
+ * Every entry point
+ *   - takes raw device pointers that the caller allocated (the library never
+ *     allocates device memory, except where a workspace is passed in),
+ *   - takes element counts / shapes as int64 for contiguous row-major data,
+ *   - enqueues its kernels asynchronously on `stream` (a hipStream_t; NULL is
+ *     the legacy default stream) and never synchronises the host,
+ *   - returns 0 on success, a positive hipError_t code if a launch failed, or
+ *     a negative TILEOPS_E* code when an argument is rejected before any launch.
+ * tileops_error_string() turns either kind of code into a message.
+ *
+ * Citations name the reference (Yihuace/tile-ascendnpu-ops) interface each
+ * entry point replaces; paths are relative to examples/TileOPs/.
+ */
+#ifndef TILEOPS_HIP_H
+#define TILEOPS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (torch.float32 / float16 / bfloat16). */
+enum tileops_dtype {
+  TILEOPS_F32 = 0,
+  TILEOPS_F16 = 1,
+  TILEOPS_BF16 = 2,
+};
+
+/* Unary activation / clamp selector for tileops_unary_fwd. */
+enum tileops_unary_op {
+  TILEOPS_HARDSWISH = 0,
+  TILEOPS_HARDSIGMOID = 1,
+  TILEOPS_CLAMP = 2,
+};
+
+/* Float predicate selector for tileops_isfp_fwd. */
+enum tileops_predicate {
+  TILEOPS_ISNAN = 0,
+  TILEOPS_ISINF = 1,
+  TILEOPS_ISFINITE = 2,
+};
+
+/* Flags for tileops_unary_fwd (TILEOPS_CLAMP only). */
+#define TILEOPS_CLAMP_HAS_MIN 1
+#define TILEOPS_CLAMP_HAS_MAX 2
+
+/* Argument-rejection codes (negative, so they never collide with hipError_t). */
+#define TILEOPS_EINVAL (-1)   /* bad dtype, op selector, or flag combination */
+#define TILEOPS_ESHAPE (-2)   /* negative / unsupported size */
+#define TILEOPS_ENULL (-3)    /* NULL pointer with a non-empty size */
+#define TILEOPS_EWORKSPACE (-4) /* workspace missing or too small */
+
+/* Library ABI version (major * 100 + minor). */
+int tileops_version(void);
+
+/* Message for a return code of any entry point (static storage). */
+const char* tileops_error_string(int code);
+
+/*
+ * y[i] = f(x[i]) for i < n, computed in fp32 and rounded once to `dtype`.
+ *   TILEOPS_HARDSWISH   x * min(max(x + 3, 0), 6) / 6
+ *   TILEOPS_HARDSIGMOID min(max(x + 3, 0), 6) / 6
+ *   TILEOPS_CLAMP       min(max(x, lo), hi) with the bounds selected by
+ *                       `flags` (TILEOPS_CLAMP_HAS_MIN / _HAS_MAX, at least
+ *                       one); a NaN bound yields NaN everywhere.
+ * NaN inputs propagate.  x and y may alias (in-place).
+ * Replaces HardswishFwdKernel.forward
+ * (tileops/kernels/elementwise/hardswish/hardswish.py:145-156),
+ * HardsigmoidFwdKernel.forward
+ * (tileops/kernels/elementwise/hardsigmoid/hardsigmoid.py:147) and
+ * ClampScalarFwdKernel.forward
+ * (tileops/kernels/elementwise/clamp_scalar/clamp_scalar.py:174-190).
+ */
+int tileops_unary_fwd(int op, const void* x, void* y, int64_t n, int dtype,
+                      float lo, float hi, int flags, void* stream);
+
+/*
+ * y[i] = pred(x[i]) as one byte 0/1 (torch.bool storage), i < n.
+ * Replaces IsnanFwdKernel.forward (tileops/kernels/elementwise/isnan/isnan.py:142-156),
+ * IsinfFwdKernel.forward (tileops/kernels/elementwise/isinf/isinf.py:150) and
+ * IsfiniteFwdKernel.forward (tileops/kernels/elementwise/isfinite/isfinite.py:149).
+ */
+int tileops_isfp_fwd(int pred, const void* x, uint8_t* y, int64_t n, int dtype,
+                     void* stream);
+
+/*
+ * Fused gated GELU over x[M, 2N] (gate = x[:, :N], value = x[:, N:]):
+ *   approx == 0: y = 0.5 * g * (1 + erf(g / sqrt(2))) * v
+ *   approx == 1: y = 0.5 * g * (1 + tanh(sqrt(2/pi) * (g + 0.044715 g^3))) * v
+ * fp32 math, one rounding to `dtype`; y is [M, N].
+ * Replaces GeluAndMulFwdKernel.forward
+ * (tileops/kernels/elementwise/gelu_and_mul/gelu_and_mul.py:140-147) and
+ * GeluTanhAndMulFwdKernel.forward
+ * (tileops/kernels/elementwise/gelu_tanh_and_mul/gelu_tanh_and_mul.py:143).
+ */
+int tileops_gated_gelu_fwd(int approx, const void* x, void* y, int64_t M, int64_t N,
+                           int dtype, void* stream);
+
+/*
+ * Per row m < M of N elements:
+ *   r_out = round_dtype(x + residual)
+ *   y     = round_dtype((r_out - mean) * rsqrt(var + eps) * w + b)
+ * with biased variance of the rounded sum, fp32 statistics.  x, residual,
+ * y, r_out are `dtype`; w and b are `wdtype` (the same as `dtype`, or
+ * TILEOPS_F32).
+ * Replaces FusedAddLayerNormKernel.forward
+ * (tileops/kernels/norm/fused_add_layer_norm/fused_add_layer_norm.py:131-159).
+ */
+int tileops_fused_add_layernorm_fwd(const void* x, const void* residual,
+                                    const void* w, const void* b, void* y,
+                                    void* r_out, int64_t M, int64_t N, float eps,
+                                    int dtype, int wdtype, void* stream);
+
+/*
+ * y[m] = log(sum_j exp(x[m, j])) over rows of N, fp32 accumulation, rounded
+ * to `dtype`.  A row whose maximum is +-inf gives that infinity; NaN
+ * propagates.
+ * Replaces the npub::logsumexp_fwd custom op called by LogSumExpKernel.forward
+ * (tileops/kernels/reduction/logsumexp/logsumexp.py:115-132, 321-336).
+ */
+int tileops_logsumexp_fwd(const void* x, void* y, int64_t M, int64_t N, int dtype,
+                          void* stream);
+
+/*
+ * y[m] = index (int64) of the first maximum (is_min == 0) or first minimum
+ * (is_min != 0) of row m of N elements; NaN counts as the extreme value, and
+ * among equal values the lowest index wins (torch.argmax / argmin).
+ * Replaces the npub::argreduce_fwd custom op called by ArgreduceKernel.forward
+ * (tileops/kernels/reduction/argmax/argmax.py:67-76, 195-219).
+ */
+int tileops_argreduce_fwd(const void* x, int64_t* y, int64_t M, int64_t N, int dtype,
+                          int is_min, void* stream);
+
+/*
+ * Flash attention forward, BSHD layout.
+ *   q:    [B, Sq,  H,   D]    k, v: [B, Skv, Hkv, D]   (dtype F16 or BF16)
+ *   o:    [B, Sq,  H,   D]    lse:  [B, H, Sq] float32 (log2 domain:
+ *                               logsumexp(scale * q k^T, masked) / ln 2)
+ * Causal masking is right-aligned: query i sees keys j <= i + (Skv - Sq).
+ * H % Hkv == 0 (grouped-query sharing); D must be 64 or 128.
+ * Replaces the npub::gqa_prefill_fwd_wrapped_kernel custom op called by
+ * GQAPrefillFwdKernel.forward
+ * (tileops/kernels/attention/multi_head_attention/multi_head_attention.py:77-124, 255-).
+ */
+int tileops_mha_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                    int64_t B, int64_t Sq, int64_t Skv, int64_t H, int64_t Hkv,
+                    int64_t D, int causal, float scale, int dtype, void* stream);
+
+/*
+ * Chunked gated delta rule (gated DeltaNet) prefill, per (b, h):
+ *   S_t = exp(g_t) S_{t-1} + beta_t k_t (v_t - k_t^T exp(g_t) S_{t-1})^T
+ *   o_t = scale * q_t^T S_t
+ * q, k: [B, T, H, K]  v: [B, T, H, V]  (BF16)   g, beta: [B, T, H] (F32,
+ * g is the log-decay)   h0: [B, H, K, V] F32 or NULL (zero state)
+ * o: [B, T, H, V] BF16   hT: [B, H, K, V] F32 (final state).
+ * K and V must be 128; chunk must be 64.  `ws` is a device workspace of at
+ * least tileops_gdn_prefill_workspace_bytes(...) bytes.
+ * No reference kernel exists (GatedDeltaNetPrefillFwdOp was not delivered,
+ * MIGRATION_INDEX.md:28); the recurrence follows golden_gdn_sequential
+ * (examples/gdn_prefill/probe/gdn_prefill_probe.py:60-77) and the chunked
+ * form of examples/gdn_prefill/DESIGN.md:6-17.
+ */
+int tileops_gdn_prefill_fwd(const void* q, const void* k, const void* v,
+                            const float* g, const float* beta, const float* h0,
+                            void* o, float* hT, int64_t B, int64_t T, int64_t H,
+                            int64_t K, int64_t V, int64_t chunk, float scale,
+                            int dtype, void* ws, size_t ws_bytes, void* stream);
+
+size_t tileops_gdn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K,
+                                           int64_t V, int64_t chunk);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILEOPS_HIP_H */

@@ -1,0 +1,291 @@
+"""Pin the CPU oracle before trusting it (runs without a GPU).
+
+Each oracle function is checked against an independent source:
+  * torch's CPU library routines (the reference programs call them),
+  * exhaustive enumerations where the domain is small (every fp16 / bf16
+    bit pattern for the predicates and the bf16 rounding),
+  * the boundary cases of the reference kernels' own harnesses
+    (hardswish_fwd_kernel.py:267-337, _logsumexp_kernel_single.py:215-224),
+  * closed forms (uniform attention, delta-rule invariants),
+chosen so that a dropped term, a wrong sign or a transposed operand fails.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import tileops_oracle as orc
+
+DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+
+
+def _special_f32(n=4096, sigma=3.0, seed=0):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(n) * sigma).astype(np.float32)
+    x[:24] = [0.0, -0.0, 3.0, -3.0, 6.0, -6.0, 2.999, -2.999, 1e-40, -1e-40, np.inf,
+              -np.inf, np.nan, 65504.0, -65504.0, 3.4e38, -3.4e38, 1e-8, 0.5, -0.5,
+              1.0, -1.0, 2.0, -2.0]
+    return x
+
+
+def _as_storage(x, dtype):
+    return orc.round_to(dtype, x)
+
+
+# -- storage rounding -------------------------------------------------------------
+def test_bf16_round_matches_torch_on_all_upper_patterns():
+    # every bf16 value plus values half-way between neighbours (ties to even)
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    vals = np.concatenate([hi, hi | 0x8000, hi | 0x7FFF, hi | 0x8001, hi | 0x1234])
+    f = vals.view(np.float32)
+    ref = torch.from_numpy(f.copy()).to(torch.bfloat16).float().numpy()
+    got = orc.bf16_round(f)
+    same = (got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref))
+    assert same.all()
+
+
+def test_fp16_round_matches_torch():
+    x = _special_f32(1 << 16)
+    ref = torch.from_numpy(x).half().float().numpy()
+    np.testing.assert_array_equal(orc.round_to("float16", x), ref)
+
+
+# -- unary activations ---------------------------------------------------------------
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("name", ["hardswish", "hardsigmoid"])
+def test_activation_matches_torch_bitwise(name, dtype):
+    x = _as_storage(_special_f32(), dtype)
+    fn = F.hardswish if name == "hardswish" else F.hardsigmoid
+    ref = fn(torch.from_numpy(x)).to(DTYPES[dtype]).float().numpy()
+    got = getattr(orc, name)(x, dtype)
+    np.testing.assert_array_equal(got, ref)  # NaN == NaN for assert_array_equal
+
+
+def test_hardswish_boundary_cases():
+    # reference harness: 0 -> 0, -3 -> -0.0, saturation, NaN / inf mapping
+    x = np.array([0.0, -3.0, 3.0, 4.0, -4.0, 1.5, np.nan, np.inf, -np.inf], np.float32)
+    y = orc.hardswish(x, "float32")
+    assert y[0] == 0.0 and not np.signbit(y[0])
+    assert y[1] == 0.0 and np.signbit(y[1])
+    assert y[2] == 3.0 and y[3] == 4.0 and y[4] == 0.0
+    assert y[5] == np.float32(1.5) * np.float32(4.5) / np.float32(6)
+    assert np.isnan(y[6]) and y[7] == np.inf and np.isnan(y[8])
+    s = orc.hardsigmoid(np.array([-3.0, 3.0, 0.0, np.nan, -np.inf, np.inf], np.float32), "float32")
+    np.testing.assert_array_equal(s[:3], [0.0, 1.0, 0.5])
+    assert np.isnan(s[3]) and s[4] == 0.0 and s[5] == 1.0
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize(
+    "lo, hi", [(-0.5, 0.5), (None, 0.5), (-0.5, None), (-1.0, 1.0), (2.0, 1.0), (math.nan, 1.0),
+               (0.0, math.nan)]
+)
+def test_clamp_matches_torch(dtype, lo, hi):
+    x = _as_storage(_special_f32(), dtype)
+    ref = torch.clamp(torch.from_numpy(x), lo, hi).to(DTYPES[dtype]).float().numpy()
+    np.testing.assert_array_equal(orc.clamp_scalar(x, dtype, lo, hi), ref)
+
+
+def test_clamp_requires_a_bound():
+    with pytest.raises(ValueError, match="present"):
+        orc.clamp_scalar(np.zeros(4, np.float32), "float32")
+
+
+# -- predicates: every fp16 / bf16 encoding, fp32 special encodings ------------------
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_predicates_exhaustive_half(dtype):
+    bits = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16)
+    x = bits.view(dtype)
+    xf = x.float().numpy()
+    for name in ("isnan", "isinf", "isfinite"):
+        ref = getattr(torch, name)(x).numpy()
+        np.testing.assert_array_equal(getattr(orc, name)(xf), ref)
+
+
+def test_predicates_fp32_encodings():
+    enc = np.array([0x7F800000, 0xFF800000, 0x7F800001, 0xFFC00000, 0x7FC00000, 0x7FFFFFFF,
+                    0x00000001, 0x80000000, 0x7F7FFFFF, 0x3F800000], np.uint32)
+    x = enc.view(np.float32)
+    for name in ("isnan", "isinf", "isfinite"):
+        ref = getattr(torch, name)(torch.from_numpy(x.copy())).numpy()
+        np.testing.assert_array_equal(getattr(orc, name)(x), ref)
+
+
+# -- gated GELU ------------------------------------------------------------------------
+@pytest.mark.parametrize("approx", ["none", "tanh"])
+def test_gated_gelu_matches_torch_gelu(approx):
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((64, 2 * 96)) * 2).astype(np.float32)
+    xt = torch.from_numpy(x)
+    ref = (F.gelu(xt[:, :96], approximate=approx) * xt[:, 96:]).numpy()
+    fn = orc.gelu_and_mul if approx == "none" else orc.gelu_tanh_and_mul
+    np.testing.assert_allclose(fn(x, "float32"), ref, rtol=2e-6, atol=2e-6)
+
+
+def test_gated_gelu_closed_forms():
+    g = np.array([0.0, 8.0, -8.0, 1.0], np.float32)
+    x = np.concatenate([g, np.full(4, 2.0, np.float32)])[None, :]
+    y = orc.gelu_and_mul(x, "float32")[0]
+    assert y[0] == 0.0 and y[1] == 16.0 and abs(y[2]) < 1e-12
+    # gelu(1) = 0.5 (1 + erf(1/sqrt 2)) = Phi(1) = 0.8413447460685429
+    assert abs(y[3] - 2 * 0.8413447460685429) < 1e-6
+    yt = orc.gelu_tanh_and_mul(x, "float32")[0]
+    assert yt[0] == 0.0 and yt[1] == 16.0 and abs(yt[2]) < 1e-10
+    # 0.5 (1 + tanh(sqrt(2/pi) (1 + 0.044715)))
+    assert abs(yt[3] - 2 * 0.8411919906082768) < 1e-6
+
+
+# -- fused add + LayerNorm ------------------------------------------------------------
+@pytest.mark.parametrize("dtype", list(DTYPES))
+def test_layer_norm_matches_torch(dtype):
+    rng = np.random.default_rng(2)
+    m, n = 16, 1152
+    x = _as_storage(rng.standard_normal((m, n)).astype(np.float32), dtype)
+    r = _as_storage(rng.standard_normal((m, n)).astype(np.float32), dtype)
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    y, added = orc.fused_add_layer_norm(x, r, w, b, 1e-5, dtype)
+    tdt = DTYPES[dtype]
+    added_ref = (torch.from_numpy(x) + torch.from_numpy(r)).to(tdt)
+    y_ref = F.layer_norm(added_ref.float(), (n,), torch.from_numpy(w), torch.from_numpy(b), 1e-5)
+    np.testing.assert_array_equal(added, added_ref.float().numpy())
+    tol = {"float32": 1e-5, "float16": 1e-3, "bfloat16": 1.6e-2}[dtype]
+    np.testing.assert_allclose(y, y_ref.to(tdt).float().numpy(), rtol=tol, atol=tol)
+
+
+def test_layer_norm_constant_row():
+    # a constant row has zero variance: y = b exactly (rstd finite through eps)
+    x = np.full((1, 64), 3.0, np.float32)
+    y, added = orc.fused_add_layer_norm(x, np.zeros_like(x), np.full(64, 5.0, np.float32),
+                                        np.arange(64, dtype=np.float32), 1e-5, "float32")
+    np.testing.assert_array_equal(added, x)
+    np.testing.assert_allclose(y[0], np.arange(64), atol=1e-6)
+
+
+# -- reductions ------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", list(DTYPES))
+def test_logsumexp_matches_torch(dtype):
+    rng = np.random.default_rng(3)
+    x = _as_storage((rng.standard_normal((33, 300)) * 2).astype(np.float32), dtype)
+    x[0] = -np.inf
+    x[1, 5] = np.inf
+    x[2, 7] = np.nan
+    x[3, :] = 88.0
+    ref = torch.logsumexp(torch.from_numpy(x), dim=-1).to(DTYPES[dtype]).float().numpy()
+    got = orc.logsumexp(x, dtype)
+    assert got[0] == -np.inf and got[1] == np.inf and np.isnan(got[2])
+    tol = {"float32": 1e-6, "float16": 1e-3, "bfloat16": 1.6e-2}[dtype]
+    np.testing.assert_allclose(got, ref, rtol=tol, atol=tol)
+    # closed form: a constant row c of length n -> c + ln n
+    assert abs(orc.logsumexp(np.full((1, 300), 2.0, np.float32), "float32")[0]
+               - (2.0 + math.log(300))) < 1e-6
+
+
+@pytest.mark.parametrize("is_min", [False, True])
+def test_argreduce_matches_torch(is_min):
+    rng = np.random.default_rng(4)
+    x = rng.integers(-3, 4, size=(64, 97)).astype(np.float32)  # many ties
+    x[0] = -np.inf
+    x[1, [10, 40]] = np.nan
+    x[2, :] = 0.0
+    x[2, 5] = -0.0
+    x[3, 50] = np.inf
+    x[4, 60] = -np.inf
+    t = torch.from_numpy(x)
+    ref = (t.argmin(dim=-1) if is_min else t.argmax(dim=-1)).numpy()
+    np.testing.assert_array_equal(orc.argreduce(x, -1, is_min), ref)
+    assert orc.argreduce(x, -1, is_min)[1] == 10
+
+
+def test_argmax_other_axis_and_flat():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 8, 16)).astype(np.float32)
+    np.testing.assert_array_equal(orc.argreduce(x, 0), torch.from_numpy(x).argmax(0).numpy())
+    assert orc.argreduce(x.reshape(1, -1), -1)[0] == torch.from_numpy(x).argmax().item()
+
+
+# -- attention -----------------------------------------------------------------------
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_matches_sdpa(causal):
+    rng = np.random.default_rng(6)
+    B, S, H, D = 2, 40, 3, 16
+    q, k, v = (rng.standard_normal((B, S, H, D)).astype(np.float32) for _ in range(3))
+    o, lse = orc.mha_fwd(q, k, v, causal, "float32")
+    tq, tk, tv = (torch.from_numpy(a).double().transpose(1, 2) for a in (q, k, v))
+    ref = F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal).transpose(1, 2)
+    np.testing.assert_allclose(o, ref.float().numpy(), rtol=1e-5, atol=1e-6)
+    s = (tq @ tk.transpose(-1, -2)) * D**-0.5
+    if causal:
+        s = s.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), -math.inf)
+    lse_ref = torch.logsumexp(s, -1) / math.log(2.0)
+    np.testing.assert_allclose(lse, lse_ref.float().numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_mha_uniform_attention_closed_form():
+    # q = 0 -> every visible key has weight 1/n: o = running mean of v, lse = log2(n)
+    B, S, H, D = 1, 9, 1, 4
+    q = np.zeros((B, S, H, D), np.float32)
+    k = np.ones((B, S, H, D), np.float32)
+    v = np.arange(S * D, dtype=np.float32).reshape(B, S, H, D)
+    o, lse = orc.mha_fwd(q, k, v, True, "float32")
+    for i in range(S):
+        np.testing.assert_allclose(o[0, i, 0], v[0, : i + 1, 0].mean(0), rtol=1e-6)
+        assert abs(lse[0, 0, i] - math.log2(i + 1)) < 1e-6
+    o, lse = orc.mha_fwd(q, k, v, False, "float32")
+    np.testing.assert_allclose(o[0, :, 0], np.broadcast_to(v[0, :, 0].mean(0), (S, D)), rtol=1e-6)
+
+
+# -- gated delta rule -----------------------------------------------------------------
+def _gdn_inputs(B=2, T=37, H=2, K=8, V=6, seed=7, h0=True):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, T, H, K))
+    k = rng.standard_normal((B, T, H, K))
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    v = rng.standard_normal((B, T, H, V))
+    g = np.log(1 / (1 + np.exp(-rng.standard_normal((B, T, H)))))  # logsigmoid
+    beta = 1 / (1 + np.exp(-rng.standard_normal((B, T, H))))
+    s0 = rng.standard_normal((B, H, K, V)) if h0 else None
+    return q, k, v, g, beta, s0
+
+
+@pytest.mark.parametrize("chunk", [4, 16, 64])
+def test_gdn_sequential_equals_chunked(chunk):
+    q, k, v, g, beta, s0 = _gdn_inputs()
+    o1, s1 = orc.gdn_sequential(q, k, v, g, beta, s0, 0.3)
+    o2, s2 = orc.gdn_chunked(q, k, v, g, beta, s0, 0.3, chunk=chunk)
+    np.testing.assert_allclose(o1, o2, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(s1, s2, rtol=1e-5, atol=1e-5)
+
+
+def test_gdn_beta_zero_only_decays():
+    q, k, v, g, beta, s0 = _gdn_inputs()
+    beta[:] = 0.0
+    o, s = orc.gdn_sequential(q, k, v, g, beta, s0, 0.5)
+    cum = np.cumsum(g, axis=1)  # [B, T, H]
+    np.testing.assert_allclose(s, np.exp(cum[:, -1])[:, :, None, None] * s0, rtol=1e-5)
+    expect = 0.5 * np.einsum("bthk,bhkv->bthv", q, s0) * np.exp(cum)[..., None]
+    np.testing.assert_allclose(o, expect, rtol=1e-4, atol=1e-5)
+
+
+def test_gdn_delta_rule_writes_values():
+    # g = 0, beta = 1, orthonormal keys: the state maps each key to its value
+    K = V = 8
+    T = 6
+    keys = np.linalg.qr(np.random.default_rng(8).standard_normal((K, K)))[0][:T]
+    k = keys[None, :, None, :]
+    v = np.random.default_rng(9).standard_normal((1, T, 1, V))
+    z = np.zeros((1, T, 1))
+    o, s = orc.gdn_sequential(k, k, v, z, np.ones((1, T, 1)), None, 1.0)
+    np.testing.assert_allclose(keys @ s[0, 0], v[0, :, 0], atol=1e-6)
+    np.testing.assert_allclose(o[0, :, 0], v[0, :, 0], atol=1e-6)  # q_t = k_t reads v_t
+
+
+def test_gdn_empty_sequence_passes_state_through():
+    q, k, v, g, beta, s0 = _gdn_inputs(T=0)
+    o, s = orc.gdn_sequential(q, k, v, g, beta, s0, 1.0)
+    assert o.shape == (2, 0, 2, 6)
+    np.testing.assert_allclose(s, s0, rtol=1e-6)

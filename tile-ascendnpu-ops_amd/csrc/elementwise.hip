@@ -1,0 +1,399 @@
+// Memory-bound elementwise kernels for gfx950:
+//   * unary activations / clamp           (tileops_unary_fwd)
+//   * float predicates -> bool bytes      (tileops_isfp_fwd)
+//   * fused gated GELU (erf and tanh)     (tileops_gated_gelu_fwd)
+//
+// All three stream HBM with 128-bit non-temporal loads/stores: every lane
+// moves whole 16-byte packs, each thread keeps several packs in flight
+// before it computes (loads are batched ahead of the math), and the math is
+// fp32 with a single rounding back to the storage type.
+#include "common.h"
+
+namespace tileops {
+
+// ---------------------------------------------------------------------------
+// Unary activations.  Comparisons are written so that a NaN input falls
+// through every select unchanged (NaN < a and NaN > a are both false), which
+// gives torch's NaN propagation without a separate isnan test; fmaxf/fminf
+// are avoided because they drop NaN.
+// ---------------------------------------------------------------------------
+template <int OP>
+__device__ __forceinline__ float unary_op(float x, float lo, float hi, int flags) {
+  if constexpr (OP == TILEOPS_HARDSWISH) {
+    // x * min(max(x + 3, 0), 6) / 6  (F.hardswish; test_hardswish.py:38-39)
+    float t = x + 3.0f;
+    t = t < 0.0f ? 0.0f : t;
+    t = t > 6.0f ? 6.0f : t;
+    return x * t / 6.0f;
+  } else if constexpr (OP == TILEOPS_HARDSIGMOID) {
+    // min(max(x + 3, 0), 6) / 6  (F.hardsigmoid; test_hardsigmoid.py:38-39)
+    float t = x + 3.0f;
+    t = t < 0.0f ? 0.0f : t;
+    t = t > 6.0f ? 6.0f : t;
+    return t / 6.0f;
+  } else {
+    // torch.clamp(x, min, max) (test_clamp_scalar.py:56-57): NaN input stays
+    // NaN; a NaN bound selects the bound itself, i.e. NaN everywhere; with
+    // min > max every value ends at max.
+    float y = x;
+    if (flags & TILEOPS_CLAMP_HAS_MIN) y = (y < lo || lo != lo) ? lo : y;
+    if (flags & TILEOPS_CLAMP_HAS_MAX) y = (y > hi || hi != hi) ? hi : y;
+    return y;
+  }
+}
+
+template <typename T, int OP, int UNROLL>
+__global__ __launch_bounds__(256) void unary_vec_kernel(const T* __restrict__ x,
+                                                        T* __restrict__ y, int64_t npack,
+                                                        float lo, float hi, int flags) {
+  constexpr int V = Elem<T>::kVec;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; base < npack;
+       base += stride * UNROLL) {
+    Pack<T> in[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t i = base + u * stride;
+      if (i < npack) in[u] = load_pack_nt(x + i * V);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t i = base + u * stride;
+      if (i < npack) {
+        Pack<T> out;
+#pragma unroll
+        for (int e = 0; e < V; ++e)
+          out.v[e] = Elem<T>::from_f32(unary_op<OP>(Elem<T>::to_f32(in[u].v[e]), lo, hi, flags));
+        store_pack_nt(y + i * V, out);
+      }
+    }
+  }
+}
+
+// Scalar path: tails after the packed body, and misaligned tensors.
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void unary_scalar_kernel(const T* __restrict__ x,
+                                                           T* __restrict__ y, int64_t begin,
+                                                           int64_t n, float lo, float hi,
+                                                           int flags) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = Elem<T>::from_f32(unary_op<OP>(Elem<T>::to_f32(x[i]), lo, hi, flags));
+}
+
+template <typename T, int OP>
+static int launch_unary(const void* xv, void* yv, int64_t n, float lo, float hi, int flags,
+                        hipStream_t s) {
+  constexpr int V = Elem<T>::kVec;
+  constexpr int UNROLL = 4;
+  const T* x = static_cast<const T*>(xv);
+  T* y = static_cast<T*>(yv);
+  int64_t npack = (host_aligned16(x) && host_aligned16(y)) ? n / V : 0;
+  if (npack > 0) {
+    int64_t grid = stream_grid((npack + UNROLL - 1) / UNROLL, 256);
+    unary_vec_kernel<T, OP, UNROLL><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, y, npack, lo,
+                                                                               hi, flags);
+  }
+  int64_t done = npack * V;
+  if (done < n) {
+    int64_t grid = stream_grid(n - done, 256);
+    unary_scalar_kernel<T, OP><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, y, done, n, lo, hi,
+                                                                          flags);
+  }
+  return launch_status();
+}
+
+template <typename T>
+static int dispatch_unary(int op, const void* x, void* y, int64_t n, float lo, float hi,
+                          int flags, hipStream_t s) {
+  switch (op) {
+    case TILEOPS_HARDSWISH: return launch_unary<T, TILEOPS_HARDSWISH>(x, y, n, lo, hi, flags, s);
+    case TILEOPS_HARDSIGMOID:
+      return launch_unary<T, TILEOPS_HARDSIGMOID>(x, y, n, lo, hi, flags, s);
+    case TILEOPS_CLAMP: return launch_unary<T, TILEOPS_CLAMP>(x, y, n, lo, hi, flags, s);
+  }
+  return TILEOPS_EINVAL;
+}
+
+// ---------------------------------------------------------------------------
+// Float predicates.  Pure bit tests on the IEEE encoding, so the result is
+// exact for every input including signalling NaNs and subnormals:
+//   NaN:    |bits| >  exponent-all-ones
+//   inf:    |bits| == exponent-all-ones
+//   finite: exponent field != all ones
+// Each thread turns 16 inputs into one 16-byte store of 0/1 bytes.
+// ---------------------------------------------------------------------------
+template <typename T> struct FpBits;
+template <> struct FpBits<float> {
+  typedef uint32_t U;
+  static constexpr U kAbs = 0x7fffffffu, kExp = 0x7f800000u;
+};
+template <> struct FpBits<f16> {
+  typedef uint16_t U;
+  static constexpr U kAbs = 0x7fffu, kExp = 0x7c00u;
+};
+template <> struct FpBits<bf16> {
+  typedef uint16_t U;
+  static constexpr U kAbs = 0x7fffu, kExp = 0x7f80u;
+};
+
+template <typename T, int PRED>
+__device__ __forceinline__ uint32_t pred_bit(typename FpBits<T>::U b) {
+  typedef FpBits<T> F;
+  const typename F::U a = b & F::kAbs;
+  if constexpr (PRED == TILEOPS_ISNAN) return a > F::kExp ? 1u : 0u;
+  else if constexpr (PRED == TILEOPS_ISINF) return a == F::kExp ? 1u : 0u;
+  else return (b & F::kExp) != F::kExp ? 1u : 0u;
+}
+
+template <typename T, int PRED, int UNROLL>
+__global__ __launch_bounds__(256) void isfp_vec_kernel(const T* __restrict__ x,
+                                                       uint8_t* __restrict__ y, int64_t ngroup) {
+  typedef typename FpBits<T>::U U;
+  constexpr int P = 16 / Elem<T>::kVec;  // 16-byte packs per 16-element group
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; base < ngroup;
+       base += stride * UNROLL) {
+    u32x4 in[UNROLL][P];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t g = base + u * stride;
+      if (g < ngroup) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(x + g * 16);
+#pragma unroll
+        for (int p = 0; p < P; ++p) in[u][p] = __builtin_nontemporal_load(src + p);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t g = base + u * stride;
+      if (g < ngroup) {
+        const U* e = reinterpret_cast<const U*>(&in[u][0]);
+        u32x4 out;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) word |= pred_bit<T, PRED>(e[w * 4 + b]) << (8 * b);
+          out[w] = word;
+        }
+        __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(y + g * 16));
+      }
+    }
+  }
+}
+
+template <typename T, int PRED>
+__global__ __launch_bounds__(256) void isfp_scalar_kernel(const T* __restrict__ x,
+                                                          uint8_t* __restrict__ y, int64_t begin,
+                                                          int64_t n) {
+  typedef typename FpBits<T>::U U;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = (uint8_t)pred_bit<T, PRED>(reinterpret_cast<const U*>(x)[i]);
+}
+
+template <typename T, int PRED>
+static int launch_isfp(const void* xv, uint8_t* y, int64_t n, hipStream_t s) {
+  constexpr int UNROLL = 2;
+  const T* x = static_cast<const T*>(xv);
+  int64_t ngroup = (host_aligned16(x) && host_aligned16(y)) ? n / 16 : 0;
+  if (ngroup > 0) {
+    int64_t grid = stream_grid((ngroup + UNROLL - 1) / UNROLL, 256);
+    isfp_vec_kernel<T, PRED, UNROLL><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, y, ngroup);
+  }
+  int64_t done = ngroup * 16;
+  if (done < n) {
+    int64_t grid = stream_grid(n - done, 256);
+    isfp_scalar_kernel<T, PRED><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, y, done, n);
+  }
+  return launch_status();
+}
+
+template <typename T>
+static int dispatch_isfp(int pred, const void* x, uint8_t* y, int64_t n, hipStream_t s) {
+  switch (pred) {
+    case TILEOPS_ISNAN: return launch_isfp<T, TILEOPS_ISNAN>(x, y, n, s);
+    case TILEOPS_ISINF: return launch_isfp<T, TILEOPS_ISINF>(x, y, n, s);
+    case TILEOPS_ISFINITE: return launch_isfp<T, TILEOPS_ISFINITE>(x, y, n, s);
+  }
+  return TILEOPS_EINVAL;
+}
+
+// ---------------------------------------------------------------------------
+// Gated GELU.
+//
+// erf form (GeluAndMul): 0.5 * g * (1 + erf(g / sqrt(2))) * v.
+//   For half-precision storage the erf comes from Abramowitz & Stegun,
+//   Handbook of Mathematical Functions, formula 7.1.26:
+//     erf(a) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-a^2),
+//     t = 1 / (1 + p a),  a >= 0,  |error| <= 1.5e-7,
+//   extended to a < 0 by odd symmetry.  That bound is ~2^-22, far below the
+//   2^-8 / 2^-11 spacing of bf16 / fp16 results, and costs one reciprocal and
+//   one exp2 instead of the ~35 VALU instructions of the library erff, which
+//   keeps the kernel under the HBM roofline.  fp32 storage uses erff.
+// tanh form (GeluTanhAndMul): 0.5 g (1 + tanh(u)), u = sqrt(2/pi)(g + 0.044715 g^3),
+//   evaluated through the identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float erf_as7126(float x) {
+  const float a = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
+  float poly = 1.061405429f;
+  poly = fmaf(poly, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  poly *= t;
+  // exp(-a^2) = exp2(-a^2 * log2(e))
+  const float e = __builtin_amdgcn_exp2f(-(a * a) * 1.4426950408889634f);
+  const float r = fmaf(-poly, e, 1.0f);
+  return copysignf(r, x);
+}
+
+template <int APPROX, bool ACCURATE>
+__device__ __forceinline__ float gated_gelu(float g, float v) {
+  if constexpr (APPROX == 0) {
+    const float z = g * 0.7071067811865476f;
+    const float erfz = ACCURATE ? erff(z) : erf_as7126(z);
+    return 0.5f * g * (1.0f + erfz) * v;
+  } else {
+    const float u = 0.7978845608028654f * fmaf(0.044715f * g, g * g, g);
+    // 1 / (1 + exp(-2u)), exp(-2u) = exp2(-2u * log2(e))
+    const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * -2.8853900817779268f));
+    return g * s * v;
+  }
+}
+
+// One workgroup per row (grid-stride over rows); each thread owns UNROLL
+// packs of the row, issuing all gate and value loads before any math.
+template <typename T, int APPROX, int UNROLL>
+__global__ __launch_bounds__(256) void gated_gelu_vec_kernel(const T* __restrict__ x,
+                                                             T* __restrict__ y, int64_t M,
+                                                             int64_t N) {
+  constexpr int V = Elem<T>::kVec;
+  constexpr bool ACC = sizeof(T) == 4;
+  const int64_t P = N / V;  // packs per output row
+  for (int64_t row = blockIdx.y; row < M; row += gridDim.y) {
+    const T* gate = x + row * 2 * N;
+    const T* val = gate + N;
+    T* out = y + row * N;
+    for (int64_t p0 = (int64_t)blockIdx.x * blockDim.x * UNROLL + threadIdx.x; p0 < P;
+         p0 += (int64_t)gridDim.x * blockDim.x * UNROLL) {
+      Pack<T> gp[UNROLL], vp[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int64_t p = p0 + u * blockDim.x;
+        if (p < P) {
+          gp[u] = load_pack_nt(gate + p * V);
+          vp[u] = load_pack_nt(val + p * V);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int64_t p = p0 + u * blockDim.x;
+        if (p < P) {
+          Pack<T> o;
+#pragma unroll
+          for (int e = 0; e < V; ++e)
+            o.v[e] = Elem<T>::from_f32(gated_gelu<APPROX, ACC>(Elem<T>::to_f32(gp[u].v[e]),
+                                                               Elem<T>::to_f32(vp[u].v[e])));
+          store_pack_nt(out + p * V, o);
+        }
+      }
+    }
+  }
+}
+
+template <typename T, int APPROX>
+__global__ __launch_bounds__(256) void gated_gelu_scalar_kernel(const T* __restrict__ x,
+                                                                T* __restrict__ y, int64_t M,
+                                                                int64_t N) {
+  constexpr bool ACC = sizeof(T) == 4;
+  for (int64_t row = blockIdx.y; row < M; row += gridDim.y) {
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < N;
+         j += (int64_t)gridDim.x * blockDim.x) {
+      const float g = Elem<T>::to_f32(x[row * 2 * N + j]);
+      const float v = Elem<T>::to_f32(x[row * 2 * N + N + j]);
+      y[row * N + j] = Elem<T>::from_f32(gated_gelu<APPROX, ACC>(g, v));
+    }
+  }
+}
+
+template <typename T, int APPROX>
+static int launch_gated_gelu(const void* xv, void* yv, int64_t M, int64_t N, hipStream_t s) {
+  constexpr int V = Elem<T>::kVec;
+  const T* x = static_cast<const T*>(xv);
+  T* y = static_cast<T*>(yv);
+  const unsigned gy = (unsigned)(M < 65535 ? M : 65535);
+  if (N % V == 0 && host_aligned16(x) && host_aligned16(y)) {
+    constexpr int UNROLL = 2;
+    const int64_t P = N / V;
+    int64_t gx = (P + 256 * UNROLL - 1) / (256 * UNROLL);
+    gated_gelu_vec_kernel<T, APPROX, UNROLL><<<dim3((unsigned)gx, gy), dim3(256), 0, s>>>(x, y, M,
+                                                                                          N);
+  } else {
+    int64_t gx = (N + 255) / 256;
+    if (gx > 64) gx = 64;
+    gated_gelu_scalar_kernel<T, APPROX><<<dim3((unsigned)gx, gy), dim3(256), 0, s>>>(x, y, M, N);
+  }
+  return launch_status();
+}
+
+template <typename T>
+static int dispatch_gated_gelu(int approx, const void* x, void* y, int64_t M, int64_t N,
+                               hipStream_t s) {
+  if (approx == 0) return launch_gated_gelu<T, 0>(x, y, M, N, s);
+  if (approx == 1) return launch_gated_gelu<T, 1>(x, y, M, N, s);
+  return TILEOPS_EINVAL;
+}
+
+}  // namespace tileops
+
+using namespace tileops;
+
+extern "C" int tileops_unary_fwd(int op, const void* x, void* y, int64_t n, int dtype, float lo,
+                                 float hi, int flags, void* stream) {
+  if (n < 0) return TILEOPS_ESHAPE;
+  if (op == TILEOPS_CLAMP && (flags & (TILEOPS_CLAMP_HAS_MIN | TILEOPS_CLAMP_HAS_MAX)) == 0)
+    return TILEOPS_EINVAL;
+  if (op < TILEOPS_HARDSWISH || op > TILEOPS_CLAMP) return TILEOPS_EINVAL;
+  if (dtype < TILEOPS_F32 || dtype > TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (n == 0) return 0;
+  if (!x || !y) return TILEOPS_ENULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TILEOPS_F32: return dispatch_unary<float>(op, x, y, n, lo, hi, flags, s);
+    case TILEOPS_F16: return dispatch_unary<f16>(op, x, y, n, lo, hi, flags, s);
+    default: return dispatch_unary<bf16>(op, x, y, n, lo, hi, flags, s);
+  }
+}
+
+extern "C" int tileops_isfp_fwd(int pred, const void* x, uint8_t* y, int64_t n, int dtype,
+                                void* stream) {
+  if (n < 0) return TILEOPS_ESHAPE;
+  if (pred < TILEOPS_ISNAN || pred > TILEOPS_ISFINITE) return TILEOPS_EINVAL;
+  if (dtype < TILEOPS_F32 || dtype > TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (n == 0) return 0;
+  if (!x || !y) return TILEOPS_ENULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TILEOPS_F32: return dispatch_isfp<float>(pred, x, y, n, s);
+    case TILEOPS_F16: return dispatch_isfp<f16>(pred, x, y, n, s);
+    default: return dispatch_isfp<bf16>(pred, x, y, n, s);
+  }
+}
+
+extern "C" int tileops_gated_gelu_fwd(int approx, const void* x, void* y, int64_t M, int64_t N,
+                                      int dtype, void* stream) {
+  if (M < 0 || N < 0) return TILEOPS_ESHAPE;
+  if (approx != 0 && approx != 1) return TILEOPS_EINVAL;
+  if (dtype < TILEOPS_F32 || dtype > TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (M == 0 || N == 0) return 0;
+  if (!x || !y) return TILEOPS_ENULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TILEOPS_F32: return dispatch_gated_gelu<float>(approx, x, y, M, N, s);
+    case TILEOPS_F16: return dispatch_gated_gelu<f16>(approx, x, y, M, N, s);
+    default: return dispatch_gated_gelu<bf16>(approx, x, y, M, N, s);
+  }
+}

@@ -1,0 +1,218 @@
+// Fused residual add + LayerNorm for gfx950 (tileops_fused_add_layernorm_fwd).
+//
+// Semantics follow FusedAddLayerNormFwdOp's reference program
+// (tests/ops/test_fused_add_layer_norm.py:55-72):
+//   r_out = round_T(x + residual)                  stored as T
+//   y     = round_T((r_out - mean) * rstd * w + b)  mean/var of the *rounded* sum,
+//                                                   biased variance, fp32 math
+//
+// Fast path (row fits in registers, N % pack == 0, 16-byte aligned rows):
+// a persistent grid where each wavefront owns whole rows.  A lane holds KP
+// packs of the rounded sum (exactly representable in T, so it is kept packed
+// in T and costs no extra precision), the two row statistics are wavefront
+// butterflies, and w / b are staged once per workgroup into LDS as fp32 so
+// that the HBM stream is only x, residual in and y, r_out out.
+// Fallback: one workgroup per row, three passes over global memory.
+#include "common.h"
+
+namespace tileops {
+
+template <typename W>
+__device__ __forceinline__ float wload(const W* p, int64_t i) {
+  return Elem<W>::to_f32(p[i]);
+}
+
+template <typename T, typename W, int KP>
+__global__ __launch_bounds__(256) void fused_add_ln_reg_kernel(
+    const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
+    const W* __restrict__ b, T* __restrict__ y, T* __restrict__ rout, int64_t M, int N,
+    float eps) {
+  constexpr int V = Elem<T>::kVec;
+  extern __shared__ float smem[];  // w[N] then b[N], fp32
+  float* sw = smem;
+  float* sb = smem + N;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    sw[i] = wload(w, i);
+    sb[i] = wload(b, i);
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int64_t waves_total = (int64_t)gridDim.x * (blockDim.x >> 6);
+  const int npack = N / V;
+  const float inv_n = 1.0f / (float)N;
+
+  for (int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); row < M;
+       row += waves_total) {
+    const T* xr = x + row * N;
+    const T* rr = res + row * N;
+    Pack<T> xs[KP], rs[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const int p = k * 64 + lane;
+      if (p < npack) {
+        xs[k] = load_pack_nt(xr + (int64_t)p * V);
+        rs[k] = load_pack_nt(rr + (int64_t)p * V);
+      }
+    }
+    // rounded residual sum, kept in xs; its fp32 row sum
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const int p = k * 64 + lane;
+      if (p < npack) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const T s = Elem<T>::from_f32(Elem<T>::to_f32(xs[k].v[e]) + Elem<T>::to_f32(rs[k].v[e]));
+          xs[k].v[e] = s;
+          sum += Elem<T>::to_f32(s);
+        }
+        store_pack_nt(rout + row * N + (int64_t)p * V, xs[k]);
+      }
+    }
+    const float mean = wave_sum(sum) * inv_n;
+    float sq = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const int p = k * 64 + lane;
+      if (p < npack) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
+          sq = fmaf(d, d, sq);
+        }
+      }
+    }
+    const float var = wave_sum(sq) * inv_n;
+    const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const int p = k * 64 + lane;
+      if (p < npack) {
+        Pack<T> o;
+        const float* wp = sw + p * V;
+        const float* bp = sb + p * V;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
+          o.v[e] = Elem<T>::from_f32(fmaf(d * rstd, wp[e], bp[e]));
+        }
+        store_pack_nt(y + row * N + (int64_t)p * V, o);
+      }
+    }
+  }
+}
+
+// General rows: any N, any alignment.  Pass 1 writes r_out and sums it,
+// pass 2 re-reads r_out (L2-resident for one row) for the variance, pass 3
+// normalises.
+template <typename T, typename W>
+__global__ __launch_bounds__(256) void fused_add_ln_generic_kernel(
+    const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
+    const W* __restrict__ b, T* __restrict__ y, T* __restrict__ rout, int64_t M, int64_t N,
+    float eps) {
+  __shared__ float part[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int64_t row = blockIdx.x; row < M; row += gridDim.x) {
+    const T* xr = x + row * N;
+    const T* rr = res + row * N;
+    T* orow = rout + row * N;
+    float sum = 0.0f;
+    for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
+      const T s = Elem<T>::from_f32(Elem<T>::to_f32(xr[j]) + Elem<T>::to_f32(rr[j]));
+      orow[j] = s;
+      sum += Elem<T>::to_f32(s);
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) part[wave] = sum;
+    __syncthreads();
+    const float mean = (part[0] + part[1] + part[2] + part[3]) / (float)N;
+    __syncthreads();
+    float sq = 0.0f;
+    for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
+      const float d = Elem<T>::to_f32(orow[j]) - mean;
+      sq = fmaf(d, d, sq);
+    }
+    sq = wave_sum(sq);
+    if (lane == 0) part[wave] = sq;
+    __syncthreads();
+    const float var = (part[0] + part[1] + part[2] + part[3]) / (float)N;
+    __syncthreads();
+    const float rstd = 1.0f / sqrtf(var + eps);
+    for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
+      const float d = Elem<T>::to_f32(orow[j]) - mean;
+      y[row * N + j] = Elem<T>::from_f32(fmaf(d * rstd, wload(w, j), wload(b, j)));
+    }
+  }
+}
+
+template <typename T, typename W, int KP>
+static void launch_reg(const T* x, const T* r, const W* w, const W* b, T* y, T* ro, int64_t M,
+                       int N, float eps, hipStream_t s) {
+  const size_t lds = (size_t)N * 2 * sizeof(float);
+  // Persistent grid: 2 workgroups (8 wavefronts) per CU, never more
+  // wavefronts than rows.
+  int64_t blocks = 256 * 2;
+  const int64_t need = (M + 3) / 4;
+  if (blocks > need) blocks = need;
+  fused_add_ln_reg_kernel<T, W, KP><<<dim3((unsigned)blocks), dim3(256), lds, s>>>(x, r, w, b, y,
+                                                                                  ro, M, N, eps);
+}
+
+template <typename T, typename W>
+static int launch_fused_add_ln(const void* xv, const void* rv, const void* wv, const void* bv,
+                               void* yv, void* rov, int64_t M, int64_t N, float eps,
+                               hipStream_t s) {
+  constexpr int V = Elem<T>::kVec;
+  const T* x = static_cast<const T*>(xv);
+  const T* r = static_cast<const T*>(rv);
+  const W* w = static_cast<const W*>(wv);
+  const W* b = static_cast<const W*>(bv);
+  T* y = static_cast<T*>(yv);
+  T* ro = static_cast<T*>(rov);
+  const bool packable = N % V == 0 && host_aligned16(x) && host_aligned16(r) &&
+                        host_aligned16(y) && host_aligned16(ro);
+  const int64_t lane_packs = (N / V + 63) / 64;
+  if (packable && lane_packs <= 16) {
+    const int n = (int)N;
+    if (lane_packs <= 1) launch_reg<T, W, 1>(x, r, w, b, y, ro, M, n, eps, s);
+    else if (lane_packs <= 2) launch_reg<T, W, 2>(x, r, w, b, y, ro, M, n, eps, s);
+    else if (lane_packs <= 4) launch_reg<T, W, 4>(x, r, w, b, y, ro, M, n, eps, s);
+    else if (lane_packs <= 8) launch_reg<T, W, 8>(x, r, w, b, y, ro, M, n, eps, s);
+    else launch_reg<T, W, 16>(x, r, w, b, y, ro, M, n, eps, s);
+  } else {
+    int64_t blocks = M < 256 * 16 ? M : 256 * 16;
+    fused_add_ln_generic_kernel<T, W><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(x, r, w, b, y,
+                                                                                  ro, M, N, eps);
+  }
+  return launch_status();
+}
+
+template <typename T>
+static int dispatch_ln_w(const void* x, const void* r, const void* w, const void* b, void* y,
+                         void* ro, int64_t M, int64_t N, float eps, int wdtype, hipStream_t s) {
+  if (wdtype == TILEOPS_F32) return launch_fused_add_ln<T, float>(x, r, w, b, y, ro, M, N, eps, s);
+  return launch_fused_add_ln<T, T>(x, r, w, b, y, ro, M, N, eps, s);
+}
+
+}  // namespace tileops
+
+using namespace tileops;
+
+extern "C" int tileops_fused_add_layernorm_fwd(const void* x, const void* residual, const void* w,
+                                               const void* b, void* y, void* r_out, int64_t M,
+                                               int64_t N, float eps, int dtype, int wdtype,
+                                               void* stream) {
+  if (M < 0 || N <= 0 || N > INT32_MAX) return TILEOPS_ESHAPE;
+  if (dtype < TILEOPS_F32 || dtype > TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (wdtype != dtype && wdtype != TILEOPS_F32) return TILEOPS_EINVAL;
+  if (M == 0) return 0;
+  if (!x || !residual || !w || !b || !y || !r_out) return TILEOPS_ENULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TILEOPS_F32: return launch_fused_add_ln<float, float>(x, residual, w, b, y, r_out, M, N,
+                                                              eps, s);
+    case TILEOPS_F16: return dispatch_ln_w<f16>(x, residual, w, b, y, r_out, M, N, eps, wdtype, s);
+    default: return dispatch_ln_w<bf16>(x, residual, w, b, y, r_out, M, N, eps, wdtype, s);
+  }
+}

@@ -1,0 +1,101 @@
+"""FusedAddLayerNormKernel: residual add + LayerNorm in one gfx950 kernel.
+
+Reference class:
+examples/TileOPs/tileops/kernels/norm/fused_add_layer_norm/fused_add_layer_norm.py:61-159.
+Per row of N elements::
+
+    residual_out = round_dtype(x + residual)
+    y = round_dtype((residual_out - mean) * rsqrt(var + eps) * weight + bias)
+
+with mean / biased variance of the rounded sum in fp32.  ``forward`` returns a
+list ``[y, residual_out]`` shaped like ``x``.  ``weight`` / ``bias`` may be the
+input dtype (the reference contract) or float32.
+Device code: fused_add_ln_reg_kernel in csrc/norm.hip.
+"""
+
+from typing import Optional
+
+import torch
+
+from tileops import _native
+from tileops.kernels.kernel_base import Kernel
+
+__all__ = ["FusedAddLayerNormKernel"]
+
+
+class FusedAddLayerNormKernel(Kernel):
+    """Fused add + LayerNorm forward kernel.
+
+    Args:
+        M: Number of rows (product of the leading dims of ``x``).
+        N: Hidden dimension.
+        eps: Variance epsilon.
+        dtype: float32, float16 or bfloat16.
+        config: Optional config override.
+    """
+
+    supported_archs: Optional[list] = None
+    SUPPORTED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+    profile_kernel_name = "fused_add_ln"
+
+    def __init__(
+        self,
+        M: int,
+        N: int,
+        eps: float,
+        dtype: torch.dtype,
+        config: Optional[dict] = None,
+    ):
+        super().__init__()
+        if dtype not in self.SUPPORTED_DTYPES:
+            supported = ", ".join(str(dt) for dt in self.SUPPORTED_DTYPES)
+            raise ValueError(
+                f"{self.__class__.__name__} only supports dtypes [{supported}], got {dtype}"
+            )
+        self.M = M
+        self.N = N
+        self.eps = eps
+        self.dtype = dtype
+        self.init_config(config)
+
+    @property
+    def default_config(self) -> dict:
+        # one wavefront per row, row held in registers, w/b staged in LDS
+        return {"rows_per_wave": 1, "persistent_blocks_per_cu": 2}
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        residual: torch.Tensor,
+        weight: torch.Tensor,
+        bias: torch.Tensor,
+    ) -> list[torch.Tensor]:
+        _native.require_device(x, residual, weight, bias)
+        original_shape = x.shape
+        rows = x.contiguous().reshape(-1, self.N)
+        res = residual.contiguous().reshape(-1, self.N)
+        w = weight.contiguous().reshape(self.N)
+        b = bias.contiguous().reshape(self.N)
+        if w.dtype != b.dtype:
+            raise ValueError(f"weight.dtype {w.dtype} != bias.dtype {b.dtype}")
+        if w.dtype not in (self.dtype, torch.float32):
+            raise ValueError(f"weight dtype must be {self.dtype} or torch.float32, got {w.dtype}")
+        m = rows.shape[0]
+        y = torch.empty_like(rows)
+        r_out = torch.empty_like(rows)
+        code = _native.lib().tileops_fused_add_layernorm_fwd(
+            rows.data_ptr(),
+            res.data_ptr(),
+            w.data_ptr(),
+            b.data_ptr(),
+            y.data_ptr(),
+            r_out.data_ptr(),
+            m,
+            self.N,
+            float(self.eps),
+            _native.dtype_code(self.dtype),
+            _native.dtype_code(w.dtype),
+            _native.stream_of(rows),
+        )
+        _native.check(code, "FusedAddLayerNormKernel")
+        return [y.reshape(original_shape), r_out.reshape(original_shape)]
