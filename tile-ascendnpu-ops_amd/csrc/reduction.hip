@@ -18,20 +18,23 @@ constexpr float kLog2e = 1.4426950408889634f;
 // ---------------------------------------------------------------------------
 // LogSumExp: online (max, scaled-sum) per lane.
 //
-// The running max is clamped to [-FLT_MAX, FLT_MAX], which reproduces
-// torch.logsumexp's special cases without per-element tests:
+// The running max is clamped to [-kBig, kBig], which reproduces
+// torch.logsumexp's special cases without per-element tests (x - m is
+// +-inf exactly when x is, and m - m' never produces inf - inf):
 //   all -inf    -> sum 0, log 0 = -inf          (result -inf)
-//   any +inf    -> exp(+inf - FLT_MAX) = +inf   (result +inf)
+//   any +inf    -> exp(+inf - kBig) = +inf      (result +inf)
 //   any NaN     -> NaN enters the sum           (result NaN)
 // ---------------------------------------------------------------------------
 struct LseState {
-  float m;  // running max (clamped, finite)
+  float m;  // running max, clamped to [-kBig, kBig]
   float s;  // sum of exp(x - m)
 };
 
+constexpr float kBig = 2.0e38f;  // kBig * log2(e) = 2.9e38 < FLT_MAX
+
 __device__ __forceinline__ float clampf_fin(float v) {
-  v = v > FLT_MAX ? FLT_MAX : v;
-  return v < -FLT_MAX ? -FLT_MAX : v;
+  v = v > kBig ? kBig : v;
+  return v < -kBig ? -kBig : v;
 }
 
 __device__ __forceinline__ LseState lse_merge(LseState a, LseState b) {
@@ -48,10 +51,12 @@ __device__ __forceinline__ void lse_fold(LseState& st, const float (&v)[CNT]) {
 #pragma unroll
   for (int i = 1; i < CNT; ++i) bm = v[i] > bm ? v[i] : bm;
   const float mn = clampf_fin(bm > st.m ? bm : st.m);
-  const float nml = -mn * kLog2e;
-  float acc = st.s * __builtin_amdgcn_exp2f(fmaf(st.m, kLog2e, nml));
+  // exp(x - m) as exp2((x - m) * log2 e): subtracting first keeps the
+  // exponent exact for large |m| (an fma(x, log2 e, -m log2 e) would leave
+  // the rounding residue of m log2 e, ~1e31 at |m| ~ 1e38).
+  float acc = st.s * __builtin_amdgcn_exp2f((st.m - mn) * kLog2e);
 #pragma unroll
-  for (int i = 0; i < CNT; ++i) acc += __builtin_amdgcn_exp2f(fmaf(v[i], kLog2e, nml));
+  for (int i = 0; i < CNT; ++i) acc += __builtin_amdgcn_exp2f((v[i] - mn) * kLog2e);
   st.m = mn;
   st.s = acc;
 }
@@ -121,7 +126,7 @@ template <> struct RowState<2> { typedef ArgState S; };
 
 template <int OP>
 __device__ __forceinline__ typename RowState<OP>::S row_init() {
-  if constexpr (OP == 0) return LseState{-FLT_MAX, 0.0f};
+  if constexpr (OP == 0) return LseState{-kBig, 0.0f};
   else return ArgState{0.0f, -1};
 }
 
