@@ -6,12 +6,10 @@
 //   y     = round_T((r_out - mean) * rstd * w + b)  mean/var of the *rounded* sum,
 //                                                   biased variance, fp32 math
 //
-// Fast path (row fits in registers, N % pack == 0, 16-byte aligned rows):
-// a persistent grid where each wavefront owns whole rows.  A lane holds KP
-// packs of the rounded sum (exactly representable in T, so it is kept packed
-// in T and costs no extra precision), the two row statistics are wavefront
-// butterflies, and w / b are staged once per workgroup into LDS as fp32 so
-// that the HBM stream is only x, residual in and y, r_out out.
+// Fast path (N % pack == 0, 16-byte aligned rows, a row fits in 16 packs per
+// lane): one wavefront per row, the two row statistics are wavefront
+// butterflies, w / b are staged once per workgroup into LDS as fp32 so that
+// the HBM stream is only x, residual in and y, r_out out.
 // Fallback: one workgroup per row, three passes over global memory.
 #include "common.h"
 
@@ -22,8 +20,12 @@ __device__ __forceinline__ float wload(const W* p, int64_t i) {
   return Elem<W>::to_f32(p[i]);
 }
 
-template <typename T, typename W, int KP>
-__global__ __launch_bounds__(256) void fused_add_ln_reg_kernel(
+// One wavefront per row, WPB rows per workgroup (one-shot grid).  The
+// workgroup stages w / b into LDS (fp32), then each lane loads its KP packs
+// of x and residual; the rounded sum stays in registers in the storage type
+// (exactly representable, so nothing is lost).
+template <typename T, typename W, int KP, int WPB>
+__global__ __launch_bounds__(WPB * 64) void fused_add_ln_wave_kernel(
     const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
     const W* __restrict__ b, T* __restrict__ y, T* __restrict__ rout, int64_t M, int N,
     float eps) {
@@ -31,74 +33,71 @@ __global__ __launch_bounds__(256) void fused_add_ln_reg_kernel(
   extern __shared__ float smem[];  // w[N] then b[N], fp32
   float* sw = smem;
   float* sb = smem + N;
-  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+  const int lane = threadIdx.x & 63;
+  const int npack = N / V;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  const bool live = row < M;
+  const T* xr = x + row * N;
+  const T* rr = res + row * N;
+
+  for (int i = threadIdx.x; i < N; i += WPB * 64) {
     sw[i] = wload(w, i);
     sb[i] = wload(b, i);
   }
   __syncthreads();
+  if (!live) return;
+  Pack<T> xs[KP], rs[KP];
+#pragma unroll
+  for (int k = 0; k < KP; ++k) {
+    const int p = k * 64 + lane;
+    if (p < npack) {
+      xs[k] = load_pack_nt(xr + (int64_t)p * V);
+      rs[k] = load_pack_nt(rr + (int64_t)p * V);
+    }
+  }
 
-  const int lane = threadIdx.x & 63;
-  const int64_t waves_total = (int64_t)gridDim.x * (blockDim.x >> 6);
-  const int npack = N / V;
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KP; ++k) {
+    const int p = k * 64 + lane;
+    if (p < npack) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const T s = Elem<T>::from_f32(Elem<T>::to_f32(xs[k].v[e]) + Elem<T>::to_f32(rs[k].v[e]));
+        xs[k].v[e] = s;
+        sum += Elem<T>::to_f32(s);
+      }
+      store_pack_nt(rout + row * N + (int64_t)p * V, xs[k]);
+    }
+  }
   const float inv_n = 1.0f / (float)N;
-
-  for (int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); row < M;
-       row += waves_total) {
-    const T* xr = x + row * N;
-    const T* rr = res + row * N;
-    Pack<T> xs[KP], rs[KP];
+  const float mean = wave_sum(sum) * inv_n;
+  float sq = 0.0f;
 #pragma unroll
-    for (int k = 0; k < KP; ++k) {
-      const int p = k * 64 + lane;
-      if (p < npack) {
-        xs[k] = load_pack_nt(xr + (int64_t)p * V);
-        rs[k] = load_pack_nt(rr + (int64_t)p * V);
+  for (int k = 0; k < KP; ++k) {
+    const int p = k * 64 + lane;
+    if (p < npack) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
+        sq = fmaf(d, d, sq);
       }
     }
-    // rounded residual sum, kept in xs; its fp32 row sum
-    float sum = 0.0f;
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(sq) * inv_n + eps);
 #pragma unroll
-    for (int k = 0; k < KP; ++k) {
-      const int p = k * 64 + lane;
-      if (p < npack) {
+  for (int k = 0; k < KP; ++k) {
+    const int p = k * 64 + lane;
+    if (p < npack) {
+      Pack<T> o;
+      const float* wp = sw + p * V;
+      const float* bp = sb + p * V;
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const T s = Elem<T>::from_f32(Elem<T>::to_f32(xs[k].v[e]) + Elem<T>::to_f32(rs[k].v[e]));
-          xs[k].v[e] = s;
-          sum += Elem<T>::to_f32(s);
-        }
-        store_pack_nt(rout + row * N + (int64_t)p * V, xs[k]);
+      for (int e = 0; e < V; ++e) {
+        const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
+        o.v[e] = Elem<T>::from_f32(fmaf(d * rstd, wp[e], bp[e]));
       }
-    }
-    const float mean = wave_sum(sum) * inv_n;
-    float sq = 0.0f;
-#pragma unroll
-    for (int k = 0; k < KP; ++k) {
-      const int p = k * 64 + lane;
-      if (p < npack) {
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
-          sq = fmaf(d, d, sq);
-        }
-      }
-    }
-    const float var = wave_sum(sq) * inv_n;
-    const float rstd = 1.0f / sqrtf(var + eps);
-#pragma unroll
-    for (int k = 0; k < KP; ++k) {
-      const int p = k * 64 + lane;
-      if (p < npack) {
-        Pack<T> o;
-        const float* wp = sw + p * V;
-        const float* bp = sb + p * V;
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
-          o.v[e] = Elem<T>::from_f32(fmaf(d * rstd, wp[e], bp[e]));
-        }
-        store_pack_nt(y + row * N + (int64_t)p * V, o);
-      }
+      store_pack_nt(y + row * N + (int64_t)p * V, o);
     }
   }
 }
@@ -146,17 +145,16 @@ __global__ __launch_bounds__(256) void fused_add_ln_generic_kernel(
   }
 }
 
+// One-shot grid of 4-wavefront workgroups (measured best on MI355X among
+// 4 / 8 / 16 wavefronts per workgroup and workgroup-per-row variants).
 template <typename T, typename W, int KP>
-static void launch_reg(const T* x, const T* r, const W* w, const W* b, T* y, T* ro, int64_t M,
-                       int N, float eps, hipStream_t s) {
+static void launch_wave(const T* x, const T* r, const W* w, const W* b, T* y, T* ro, int64_t M,
+                        int N, float eps, hipStream_t s) {
+  constexpr int WPB = 4;
   const size_t lds = (size_t)N * 2 * sizeof(float);
-  // Persistent grid: 2 workgroups (8 wavefronts) per CU, never more
-  // wavefronts than rows.
-  int64_t blocks = 256 * 2;
-  const int64_t need = (M + 3) / 4;
-  if (blocks > need) blocks = need;
-  fused_add_ln_reg_kernel<T, W, KP><<<dim3((unsigned)blocks), dim3(256), lds, s>>>(x, r, w, b, y,
-                                                                                  ro, M, N, eps);
+  const int64_t blocks = (M + WPB - 1) / WPB;
+  fused_add_ln_wave_kernel<T, W, KP, WPB><<<dim3((unsigned)blocks), dim3(WPB * 64), lds, s>>>(
+      x, r, w, b, y, ro, M, N, eps);
 }
 
 template <typename T, typename W>
@@ -173,13 +171,13 @@ static int launch_fused_add_ln(const void* xv, const void* rv, const void* wv, c
   const bool packable = N % V == 0 && host_aligned16(x) && host_aligned16(r) &&
                         host_aligned16(y) && host_aligned16(ro);
   const int64_t lane_packs = (N / V + 63) / 64;
-  if (packable && lane_packs <= 16) {
+  if (packable && lane_packs <= 16 && M <= (int64_t)UINT32_MAX) {
     const int n = (int)N;
-    if (lane_packs <= 1) launch_reg<T, W, 1>(x, r, w, b, y, ro, M, n, eps, s);
-    else if (lane_packs <= 2) launch_reg<T, W, 2>(x, r, w, b, y, ro, M, n, eps, s);
-    else if (lane_packs <= 4) launch_reg<T, W, 4>(x, r, w, b, y, ro, M, n, eps, s);
-    else if (lane_packs <= 8) launch_reg<T, W, 8>(x, r, w, b, y, ro, M, n, eps, s);
-    else launch_reg<T, W, 16>(x, r, w, b, y, ro, M, n, eps, s);
+    if (lane_packs <= 1) launch_wave<T, W, 1>(x, r, w, b, y, ro, M, n, eps, s);
+    else if (lane_packs <= 2) launch_wave<T, W, 2>(x, r, w, b, y, ro, M, n, eps, s);
+    else if (lane_packs <= 4) launch_wave<T, W, 4>(x, r, w, b, y, ro, M, n, eps, s);
+    else if (lane_packs <= 8) launch_wave<T, W, 8>(x, r, w, b, y, ro, M, n, eps, s);
+    else launch_wave<T, W, 16>(x, r, w, b, y, ro, M, n, eps, s);
   } else {
     int64_t blocks = M < 256 * 16 ? M : 256 * 16;
     fused_add_ln_generic_kernel<T, W><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(x, r, w, b, y,
