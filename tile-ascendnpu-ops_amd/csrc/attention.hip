@@ -19,6 +19,7 @@
 // The softmax runs in the log2 domain (scores scaled by scale * log2 e); the
 // per-row LSE written out is m + log2(l), i.e. logsumexp(scale q k^T) / ln 2.
 #include <float.h>
+#include <stdlib.h>
 
 #include "common.h"
 
@@ -43,36 +44,42 @@ template <> struct Mfma<f16> {
   }
 };
 
-constexpr int BM = 128;  // query rows per workgroup
-constexpr int BN = 64;   // key rows per tile
-constexpr int kThreads = 256;
+// Lazy rescaling: the running max only moves when a tile's max exceeds it by
+// more than 2^kLazyLog2 in the exp2 domain, so P <= 2^kLazyLog2 (exact in
+// fp32 / bf16) and the O accumulator is rescaled rarely.
+constexpr float kLazyLog2 = 8.0f;
 
-// position of key row `kv` (0..63) inside an LDS row of V^T: within each
-// 16-key group the 4-key blocks are stored in the order 0, 2, 1, 3.
+// position of key group `group4` (4 keys) inside an LDS row of V^T: within
+// each 16-key group the 4-key blocks are stored in the order 0, 2, 1, 3.
 __device__ __forceinline__ int vt_pos(int group4) {
   const int j = group4 & 3;
   const int pj = (j == 1) ? 2 : (j == 2 ? 1 : j);
   return (group4 >> 2) * 16 + pj * 4;
 }
 
-template <int D> struct Smem {
+template <int D, int BN> struct Smem {
   static constexpr int KS = D + 8;   // K row stride (elements): 16 B pad
   static constexpr int VS = BN + 8;  // V^T row stride (elements): 16 B pad
   static constexpr int K_ELEMS = BN * KS;
   static constexpr int V_ELEMS = D * VS;
 };
 
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads) void mha_fwd_kernel(
+template <typename T, int D, bool CAUSAL, int WAVES, int BN>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void mha_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
     float* __restrict__ lse, int B, int Sq, int Skv, int H, int Hkv, float scale_log2, int nqb) {
   typedef typename Mfma<T>::V8 V8;
-  typedef Smem<D> SM;
+  typedef Smem<D, BN> SM;
+  constexpr int NKB = BN / 32;           // 32-key blocks per tile
+  constexpr int kThreads = WAVES * 64;
+  constexpr int BM = WAVES * 32;         // query rows per workgroup
   constexpr int KSTEPS = D / 16;         // MFMA steps over the head dim
   constexpr int DBLK = D / 32;           // 32-row blocks of O^T
   constexpr int KCHUNK = D / 8;          // 16-byte chunks per K row
   constexpr int KLOADS = BN * KCHUNK / kThreads;  // 16-byte K loads per thread
   constexpr int VGROUPS = (BN / 4) * (D / 8);     // (4 keys x 8 dims) units
+  static_assert(KLOADS * kThreads == BN * KCHUNK, "K tile must split evenly over threads");
+  static_assert(VGROUPS <= kThreads, "one V unit per thread at most");
 
   __shared__ __attribute__((aligned(16))) T k_lds[SM::K_ELEMS];
   __shared__ __attribute__((aligned(16))) T v_lds[SM::V_ELEMS];
@@ -122,9 +129,10 @@ __global__ __launch_bounds__(kThreads) void mha_fwd_kernel(
   // --- register prefetch of one K / V tile
   u32x4 kpre[KLOADS];
   u32x4 vpre[4];
+  constexpr int NG = BN / 4;    // 4-key groups per tile
   const bool v_owner = tid < VGROUPS;
-  const int vg = tid % 16;      // 4-key group (0..15)
-  const int vc = tid / 16;      // 8-dim chunk
+  const int vg = tid % NG;      // 4-key group
+  const int vc = tid / NG;      // 8-dim chunk
   auto prefetch = [&](int tile) {
     const int kv0 = tile * BN;
 #pragma unroll
@@ -172,8 +180,9 @@ __global__ __launch_bounds__(kThreads) void mha_fwd_kernel(
   f32x16 acc_o[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) acc_o[i] = f32x16{};
-  float m_run = -INFINITY;
+  float m_run = -INFINITY;  // running max of raw scores (q . k)
   float l_run = 0.0f;
+  const float lazy_raw = kLazyLog2 / scale_log2;
 
   if (ntiles > 0) prefetch(0);
   for (int t = 0; t < ntiles; ++t) {
@@ -183,65 +192,77 @@ __global__ __launch_bounds__(kThreads) void mha_fwd_kernel(
     if (t + 1 < ntiles) prefetch(t + 1);
     const int kv0 = t * BN;
 
-    // S^T = K . Q^T : two 32-key blocks
-    f32x16 acc_s[2] = {f32x16{}, f32x16{}};
+    // S^T = K . Q^T : NKB 32-key blocks, their MFMA chains interleaved
+    f32x16 acc_s[NKB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < NKB; ++kb) acc_s[kb] = f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
         const V8 a =
             *reinterpret_cast<const V8*>(k_lds + (kb * 32 + col) * SM::KS + ks * 16 + half * 8);
         acc_s[kb] = Mfma<T>::run(a, qreg[ks], acc_s[kb]);
       }
     }
 
-    // online softmax for query row qi (log2 domain)
-    const bool need_mask = (kv0 + BN > Skv) || (CAUSAL && kv0 + BN - 1 > q0 + off);
-    float tmax = -INFINITY;
+    // online softmax for query row qi: maxima in raw score units, the scale
+    // (times log2 e) folded into one FMA per score inside exp2
+    // masking only on the ragged last tile and on causal diagonal tiles
+    // (a workgroup-uniform branch, kept out of the common path)
+    if ((kv0 + BN > Skv) || (CAUSAL && kv0 + BN - 1 > q0 + off)) {
+      const int lim = CAUSAL ? min(Skv - 1, qi + off) : Skv - 1;  // last visible key
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float s = acc_s[kb][r] * scale_log2;
-        if (need_mask) {
+        for (int r = 0; r < 16; ++r) {
           const int kv = kv0 + kb * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-          if (kv >= Skv || (CAUSAL && kv > qi + off)) s = -INFINITY;
+          acc_s[kb][r] = kv > lim ? -INFINITY : acc_s[kb][r];
         }
-        acc_s[kb][r] = s;
-        tmax = fmaxf(tmax, s);
       }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    // rows with no visible key yet keep m = -inf; shift by 0 so exp2 stays 0
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
-    float psum = 0.0f;
-    V8 pb[4];
+    float tmax = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, acc_s[kb][r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const bool grow = tmax > m_run + lazy_raw;
+    if (__any(grow)) {
+      const float m_new = grow ? tmax : m_run;
+      const float alpha = m_run == -INFINITY ? 0.0f
+                                             : __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[db][r] *= alpha;
+      }
+    }
+    // rows with no visible key yet keep m = -inf: shift by 0 so exp2 -> 0
+    const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * scale_log2;
+    float psum = 0.0f;
+    V8 pb[2 * NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         // fp32 probabilities form the row sum (and the LSE); P is rounded to
         // the storage type only as the MFMA operand
-        const float p = __builtin_amdgcn_exp2f(acc_s[kb][r] - m_use);
+        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[kb][r], scale_log2, neg_mc));
         psum += p;
         pb[kb * 2 + (r >> 3)][r & 7] = (T)p;
       }
     }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc_o[db][r] *= alpha;
-    }
+    l_run += psum;
 
-    // O^T += V^T . P^T
+    // O^T += V^T . P^T (independent d-blocks interleaved)
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db) {
+    for (int ks = 0; ks < BN / 16; ++ks) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+      for (int db = 0; db < DBLK; ++db) {
         const V8 a =
             *reinterpret_cast<const V8*>(v_lds + (db * 32 + col) * SM::VS + ks * 16 + half * 8);
         acc_o[db] = Mfma<T>::run(a, pb[ks], acc_o[db]);
@@ -267,34 +288,44 @@ __global__ __launch_bounds__(kThreads) void mha_fwd_kernel(
     }
     if (half == 0)
       lse[((int64_t)bb * H + hq) * Sq + qi] =
-          l_tot > 0.0f ? m_run + __builtin_amdgcn_logf(l_tot) : -INFINITY;
+          l_tot > 0.0f ? m_run * scale_log2 + __builtin_amdgcn_logf(l_tot) : -INFINITY;
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, int WAVES, int BN>
 static int launch(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Sq,
                   int Skv, int H, int Hkv, bool causal, float scale, hipStream_t s) {
+  constexpr int BM = WAVES * 32;
   const int nqb = (Sq + BM - 1) / BM;
   const int64_t total = (int64_t)nqb * H * B;
   const float scale_log2 = scale * 1.4426950408889634f;
-  dim3 grid((unsigned)total), block(kThreads);
+  dim3 grid((unsigned)total), block(WAVES * 64);
   if (causal)
-    mha_fwd_kernel<T, D, true><<<grid, block, 0, s>>>(
+    mha_fwd_kernel<T, D, true, WAVES, BN><<<grid, block, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
         static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, scale_log2, nqb);
   else
-    mha_fwd_kernel<T, D, false><<<grid, block, 0, s>>>(
+    mha_fwd_kernel<T, D, false, WAVES, BN><<<grid, block, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
         static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, scale_log2, nqb);
   return launch_status();
+}
+
+template <typename T, int D>
+static int launch_w(const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                    int Sq, int Skv, int H, int Hkv, bool causal, float scale, hipStream_t s) {
+  // 8 wavefronts x 32 query rows, 64-key tiles: measured best on MI355X
+  // among 4 / 8 wavefronts and 64 / 128-key tiles, and among software-
+  // pipelined variants with Q in LDS and double-buffered K / V slots.
+  return launch<T, D, 8, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
 }
 
 template <typename T>
 static int dispatch_d(int D, const void* q, const void* k, const void* v, void* o, float* lse,
                       int B, int Sq, int Skv, int H, int Hkv, bool causal, float scale,
                       hipStream_t s) {
-  if (D == 128) return launch<T, 128>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
-  if (D == 64) return launch<T, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
+  if (D == 128) return launch_w<T, 128>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
+  if (D == 64) return launch_w<T, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
   return TILEOPS_ESHAPE;
 }
 
@@ -316,8 +347,7 @@ extern "C" int tileops_mha_fwd(const void* q, const void* k, const void* v, void
   if (!q || !k || !v || !o || !lse) return TILEOPS_ENULL;
   if (!host_aligned16(q) || !host_aligned16(k) || !host_aligned16(v) || !host_aligned16(o))
     return TILEOPS_EINVAL;
-  const int64_t nqb = (Sq + mha::BM - 1) / mha::BM;
-  if (nqb * H * B > (int64_t)UINT32_MAX) return TILEOPS_ESHAPE;
+  if (((Sq + 127) / 128) * H * B > (int64_t)UINT32_MAX) return TILEOPS_ESHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TILEOPS_BF16)
     return mha::dispatch_d<bf16>((int)D, q, k, v, o, lse, (int)B, (int)Sq, (int)Skv, (int)H,
