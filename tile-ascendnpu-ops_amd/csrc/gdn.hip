@@ -8,21 +8,24 @@
 // log-decay, G[l,s] = exp(gc_l - gc_s) (l >= s), A = strictly_lower(beta_l
 // G[l,s] k_l.k_s) and T = (I + A)^-1:
 //   w   = T diag(beta exp(gc)) k                 (C x K)   \  independent of S:
-//   u   = T diag(beta) v                         (C x V)    > kernel 1, fully
+//   Tu  = T diag(beta)                           (C x C)    > kernel 1, fully
 //   Aqk = scale * lower_incl(G o (q k^T))        (C x C)   /  parallel over chunks
-//   W   = u - w S                                             \
+//   W   = Tu v - w S                                          \
 //   o   = scale exp(gc) o (q S) + Aqk W                        > kernel 2, sequential
 //   S  <- exp(gc_C) S + (exp(gc_C - gc) o k)^T W              /  over chunks
 // Only differences gc_l - gc_s <= 0, gc_C - gc_l <= 0 and gc <= 0 are ever
 // exponentiated, so nothing overflows however strong the decay.
 //
-// Kernel 1 (one workgroup per chunk): K K^T and Q K^T on bf16 MFMA, the
-// 64x64 unit-lower-triangular inverse by forward substitution in fp32 (one
-// lane per column of T), then w and u on MFMA.  Results go to a workspace.
+// Kernel 1 (one workgroup per chunk, two per CU): K K^T and Q K^T on bf16
+// MFMA, the 64x64 unit-lower-triangular inverse in fp32 (32x32 diagonal
+// blocks by substitution, the off-diagonal block by two small products),
+// then w on MFMA.  -w, Tu, Aqk and gc go to a workspace.
 // Kernel 2 (one workgroup per (b, h, 32-wide slice of V), 4 wavefronts):
 // the state slice lives in MFMA accumulators (wavefront i owns key rows
-// 32i..32i+31), its bf16 copy and W are exchanged through LDS, two
-// workgroup barriers per chunk.
+// 32i..32i+31), its bf16 copy and W are exchanged through LDS.  Every
+// wavefront loads the next chunk's operands with the same instruction
+// sequence while the current chunk runs; waves 0, 1 form W (rows 0-31,
+// 32-63), waves 2, 3 the output rows.  Two workgroup barriers per chunk.
 #include "common.h"
 
 namespace tileops {
@@ -40,9 +43,9 @@ constexpr int CP = C + 8;   // LDS row stride of a transposed [*][C] tile (eleme
 constexpr float kLog2e = 1.4426950408889634f;
 
 // workspace per chunk
-constexpr size_t kWOff = 0;                                   // w   [C][DK] bf16
-constexpr size_t kUOff = kWOff + (size_t)C * DK * 2;          // u   [C][DV] bf16
-constexpr size_t kAqkOff = kUOff + (size_t)C * DV * 2;        // Aqk [C][C]  bf16
+constexpr size_t kWOff = 0;                                   // -w  [C][DK] bf16
+constexpr size_t kTuOff = kWOff + (size_t)C * DK * 2;         // Tu  [C][C]  bf16
+constexpr size_t kAqkOff = kTuOff + (size_t)C * C * 2;        // Aqk [C][C]  bf16
 constexpr size_t kGcOff = kAqkOff + (size_t)C * C * 2;        // gc  [C]     f32
 constexpr size_t kChunkBytes = kGcOff + (size_t)C * 4;
 
@@ -77,18 +80,30 @@ __device__ __forceinline__ void store_transposed4x8(bf16* dst, int stride, int d
 // ---------------------------------------------------------------------------
 // kernel 1: per-chunk preparation
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gdn_prep_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const float* __restrict__ g, const float* __restrict__ beta, uint8_t* __restrict__ ws,
-    int B, int T, int H, int NC, float scale) {
-  __shared__ __attribute__((aligned(16))) bf16 k_s[C * KP];    // k natural [c][d]
-  __shared__ __attribute__((aligned(16))) bf16 kT_s[DK * CP];  // k^T [d][c]
-  __shared__ __attribute__((aligned(16))) bf16 vT_s[DV * CP];  // v^T [d][c]
-  __shared__ __attribute__((aligned(16))) float a_s[C * (C + 4)];  // A (fp32)
-  __shared__ __attribute__((aligned(16))) bf16 tw_s[C * CP];   // T diag(beta exp(gc))
-  __shared__ __attribute__((aligned(16))) bf16 tu_s[C * CP];   // T diag(beta)
-  __shared__ float gc_s[C], beta_s[C];
-  constexpr int AS = C + 4;
+// LDS plan (two workgroups fit one CU):
+//   r0: k natural [C][KP] bf16 (K K^T)            -> T (fp32 [C][AS], inverse)
+//   r1: A^T fp32 [C][AS] (A^T[m][i] = A[i][m])    -> Tw, Tu (bf16 [C][CP] each)
+//   x_s: A21 T11 (fp32 32 x 32);  kT_s: k^T [d][c] bf16 (w);  aqk_s: Aqk bf16
+constexpr int AS = 72;  // fp32 row stride of A^T / T (288 bytes: float4-aligned rows)
+constexpr int XS = 36;  // fp32 row stride of X
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_prep_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ g,
+    const float* __restrict__ beta, uint8_t* __restrict__ ws, int B, int T, int H, int NC,
+    float scale) {
+  __shared__ __attribute__((aligned(16))) float r0[C * AS];
+  __shared__ __attribute__((aligned(16))) float r1[C * AS];
+  __shared__ __attribute__((aligned(16))) float x_s[32 * XS];
+  __shared__ __attribute__((aligned(16))) bf16 kT_s[DK * CP];
+  __shared__ __attribute__((aligned(16))) bf16 aqk_s[C * CP];
+  __shared__ float gc_s[C], beta_s[C], be_s[C];
+  static_assert(C * KP * 2 <= C * AS * 4, "k tile must fit the T region");
+  static_assert(2 * C * CP * 2 <= C * AS * 4, "Tw and Tu must fit the A region");
+  bf16* k_s = reinterpret_cast<bf16*>(r0);
+  float* t_s = r0;
+  float* at_s = r1;
+  bf16* tw_s = reinterpret_cast<bf16*>(r1);
+  bf16* tu_s = tw_s + C * CP;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -100,24 +115,22 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
   const int64_t tok_stride = (int64_t)H * DK;  // DK == DV
   uint8_t* wsc = ws + (size_t)blockIdx.x * kChunkBytes;
   bf16* w_ws = reinterpret_cast<bf16*>(wsc + kWOff);
-  bf16* u_ws = reinterpret_cast<bf16*>(wsc + kUOff);
+  bf16* tu_ws = reinterpret_cast<bf16*>(wsc + kTuOff);
   bf16* aqk_ws = reinterpret_cast<bf16*>(wsc + kAqkOff);
   float* gc_ws = reinterpret_cast<float*>(wsc + kGcOff);
 
-  // ---- stage k (natural + transposed) and v (transposed); rows past T are 0
+  // ---- stage k (natural + transposed); rows past T are 0
   {
     const int vg = tid & 15, vc = tid >> 4;  // rows 4vg..4vg+3, dims 8vc..8vc+7
-    u32x4 kr[4], vr[4];
+    u32x4 kr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 4 * vg + i;
       const int64_t off = ((int64_t)b * T + t0 + row) * tok_stride + (int64_t)h * DK + vc * 8;
       kr[i] = row < n ? *reinterpret_cast<const u32x4*>(k + off) : u32x4{0, 0, 0, 0};
-      vr[i] = row < n ? *reinterpret_cast<const u32x4*>(v + off) : u32x4{0, 0, 0, 0};
       *reinterpret_cast<u32x4*>(k_s + row * KP + vc * 8) = kr[i];
     }
     store_transposed4x8(kT_s, CP, vc * 8, 4 * vg, kr);
-    store_transposed4x8(vT_s, CP, vc * 8, 4 * vg, vr);
   }
   if (wave == 0) {
     const int64_t gi = ((int64_t)b * T + t0 + lane) * H + h;
@@ -130,12 +143,14 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
     }
     gc_s[lane] = x;
     beta_s[lane] = bt;
+    be_s[lane] = bt * exp2f_fast(x * kLog2e);
     gc_ws[lane] = x;
   }
   __syncthreads();
 
-  // ---- K K^T -> A (fp32, LDS) and Q K^T -> Aqk (bf16, workspace)
-  // 32x32 blocks (row block rb, column block cb); the upper block is zero.
+  // ---- K K^T -> A^T (fp32, LDS) and Q K^T -> Aqk (bf16, LDS), in 32x32
+  // blocks (row block rb, column block cb).  Only the strictly lower parts of
+  // the diagonal blocks and the block A21 of A are ever read back.
   if (wave < 3) {
     const int rb = wave == 0 ? 0 : 1;
     const int cb = wave == 2 ? 1 : 0;
@@ -157,73 +172,129 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
     const int cs = cb * 32 + col;
     const float gcs = gc_s[cs];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int cl = rb * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-      const float gd = cl >= cs ? exp2f_fast((gc_s[cl] - gcs) * kLog2e) : 0.0f;
-      a_s[cl * AS + cs] = cl > cs ? beta_s[cl] * gd * kk[r] : 0.0f;
-      aqk_ws[cl * C + cs] = (bf16)(scale * gd * qk[r]);
+    for (int g4 = 0; g4 < 4; ++g4) {
+      float a4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = g4 * 4 + e;
+        const int cl = rb * 32 + g4 * 8 + half * 4 + e;
+        const float gd = cl >= cs ? exp2f_fast((gc_s[cl] - gcs) * kLog2e) : 0.0f;
+        a4[e] = cl > cs ? beta_s[cl] * gd * kk[r] : 0.0f;
+        aqk_s[cl * CP + cs] = (bf16)(scale * gd * qk[r]);
+      }
+      const int cl0 = rb * 32 + g4 * 8 + half * 4;
+      *reinterpret_cast<float4*>(at_s + cs * AS + cl0) = make_float4(a4[0], a4[1], a4[2], a4[3]);
     }
   } else {
     const int cs = 32 + col;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int cl = (r >> 2) * 8 + half * 4 + (r & 3);
-      a_s[cl * AS + cs] = 0.0f;
-      aqk_ws[cl * C + cs] = (bf16)0.0f;
-    }
+    for (int r = 0; r < 16; ++r) aqk_s[((r >> 2) * 8 + half * 4 + (r & 3)) * CP + cs] = (bf16)0.0f;
   }
   __syncthreads();
 
-  // ---- T = (I + A)^-1 by forward substitution; lane j owns column j:
-  //      T[i][j] = [i == j] - sum_{m < i} A[i][m] T[m][j]
+  // ---- Aqk rows to the workspace (16-byte stores); T = (I + A)^-1, blocked:
+  // T11 = (I + A11)^-1 and T22 = (I + A22)^-1 by right-looking substitution
+  // (wave 0: lanes 0-31 own the columns of T11, lanes 32-63 those of T22;
+  // p[i] accumulates sum_m A[i][m] T[m][j]), then T21 = -T22 (A21 T11).
+#pragma unroll
+  for (int e = tid; e < C * C / 8; e += 256) {
+    const int row = e >> 3, c8 = (e & 7) * 8;
+    *reinterpret_cast<u32x4*>(aqk_ws + row * C + c8) =
+        *reinterpret_cast<const u32x4*>(aqk_s + row * CP + c8);
+  }
   if (wave == 0) {
-    float tcol[C];
+    const int base = half * 32, jl = col;
+    float p[32];
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-      float s = (i == lane) ? 1.0f : 0.0f;
+    for (int i = 0; i < 32; ++i) p[i] = 0.0f;
 #pragma unroll
-      for (int m4 = 0; m4 < i; m4 += 4) {
-        const float4 a4 = *reinterpret_cast<const float4*>(a_s + i * AS + m4);
-        s = fmaf(-a4.x, tcol[m4], s);
-        if (m4 + 1 < i) s = fmaf(-a4.y, tcol[m4 + 1], s);
-        if (m4 + 2 < i) s = fmaf(-a4.z, tcol[m4 + 2], s);
-        if (m4 + 3 < i) s = fmaf(-a4.w, tcol[m4 + 3], s);
+    for (int m = 0; m < 32; ++m) {
+      const float t = (m == jl ? 1.0f : 0.0f) - p[m];
+      t_s[(base + m) * AS + base + jl] = t;
+      const float* acol = at_s + (base + m) * AS + base;  // A[base + i][base + m], i = 0..31
+#pragma unroll
+      for (int i4 = ((m + 1) >> 2) << 2; i4 < 32; i4 += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(acol + i4);
+        if (i4 + 0 > m) p[i4 + 0] = fmaf(a4.x, t, p[i4 + 0]);
+        if (i4 + 1 > m) p[i4 + 1] = fmaf(a4.y, t, p[i4 + 1]);
+        if (i4 + 2 > m) p[i4 + 2] = fmaf(a4.z, t, p[i4 + 2]);
+        if (i4 + 3 > m) p[i4 + 3] = fmaf(a4.w, t, p[i4 + 3]);
       }
-      tcol[i] = s;
-    }
-    const float bj = beta_s[lane];
-    const float bej = bj * exp2f_fast(gc_s[lane] * kLog2e);
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-      tw_s[i * CP + lane] = (bf16)(tcol[i] * bej);
-      tu_s[i * CP + lane] = (bf16)(tcol[i] * bj);
     }
   }
   __syncthreads();
-
-  // ---- w = Tw k (C x DK), u = Tu v (C x DV): wave -> row block rb, column
-  // blocks 2 (wave & 1), 2 (wave & 1) + 1 of both products
+  const int xj = tid & 31, xi = (tid >> 5) * 4;  // this thread: rows xi..xi+3, column xj
   {
-    const int rb = wave >> 1;
+    float x0 = 0.0f, x1 = 0.0f, x2 = 0.0f, x3 = 0.0f;  // X = A21 T11
+#pragma unroll 8
+    for (int kx = 0; kx < 32; ++kx) {
+      const float4 a4 = *reinterpret_cast<const float4*>(at_s + kx * AS + 32 + xi);
+      const float tk = t_s[kx * AS + xj];
+      x0 = fmaf(a4.x, tk, x0);
+      x1 = fmaf(a4.y, tk, x1);
+      x2 = fmaf(a4.z, tk, x2);
+      x3 = fmaf(a4.w, tk, x3);
+    }
+    x_s[(xi + 0) * XS + xj] = x0;
+    x_s[(xi + 1) * XS + xj] = x1;
+    x_s[(xi + 2) * XS + xj] = x2;
+    x_s[(xi + 3) * XS + xj] = x3;
+  }
+  __syncthreads();
+  {
+    float y0 = 0.0f, y1 = 0.0f, y2 = 0.0f, y3 = 0.0f;  // T21 = -T22 X
+#pragma unroll 8
+    for (int kx = 0; kx < 32; ++kx) {
+      const float xk = x_s[kx * XS + xj];
+      y0 = fmaf(t_s[(32 + xi + 0) * AS + 32 + kx], xk, y0);
+      y1 = fmaf(t_s[(32 + xi + 1) * AS + 32 + kx], xk, y1);
+      y2 = fmaf(t_s[(32 + xi + 2) * AS + 32 + kx], xk, y2);
+      y3 = fmaf(t_s[(32 + xi + 3) * AS + 32 + kx], xk, y3);
+    }
+    t_s[(32 + xi + 0) * AS + xj] = -y0;
+    t_s[(32 + xi + 1) * AS + xj] = -y1;
+    t_s[(32 + xi + 2) * AS + xj] = -y2;
+    t_s[(32 + xi + 3) * AS + xj] = -y3;
+  }
+  __syncthreads();
+
+  // ---- Tw = T diag(beta exp(gc)), Tu = T diag(beta) in bf16 (T12 is zero)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int cb = 2 * (wave & 1) + j;
-      f32x16 aw = {}, au = {};
+  for (int e = tid; e < C * C; e += 256) {
+    const int i = e >> 6, j = e & 63;
+    const float t = (i < 32 && j >= 32) ? 0.0f : t_s[i * AS + j];
+    tw_s[i * CP + j] = (bf16)(t * be_s[j]);
+    tu_s[i * CP + j] = (bf16)(t * beta_s[j]);
+  }
+  __syncthreads();
+
+  // ---- Tu rows to the workspace; -w^T = -(k^T Tw^T): wave -> 32-row block of
+  // d; the accumulator holds 4 consecutive d of one token row l (8 bytes)
+#pragma unroll
+  for (int e = tid; e < C * C / 8; e += 256) {
+    const int row = e >> 3, c8 = (e & 7) * 8;
+    *reinterpret_cast<u32x4*>(tu_ws + row * C + c8) =
+        *reinterpret_cast<const u32x4*>(tu_s + row * CP + c8);
+  }
+  {
+    const int db = wave;
+#pragma unroll
+    for (int lb = 0; lb < 2; ++lb) {
+      f32x16 aw = {};
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks) {
-        const bf16x8 tw = ld8(tw_s + (rb * 32 + col) * CP + ks * 16 + half * 8);
-        const bf16x8 tu = ld8(tu_s + (rb * 32 + col) * CP + ks * 16 + half * 8);
-        const bf16x8 bk = ld8(kT_s + (cb * 32 + col) * CP + ks * 16 + half * 8);
-        const bf16x8 bv = ld8(vT_s + (cb * 32 + col) * CP + ks * 16 + half * 8);
-        aw = mfma(tw, bk, aw);
-        au = mfma(tu, bv, au);
+        const bf16x8 ak = ld8(kT_s + (db * 32 + col) * CP + ks * 16 + half * 8);
+        const bf16x8 btw = ld8(tw_s + (lb * 32 + col) * CP + ks * 16 + half * 8);
+        aw = mfma(ak, btw, aw);
       }
-      const int d = cb * 32 + col;
+      const int l = lb * 32 + col;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int cl = rb * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        w_ws[cl * DK + d] = (bf16)aw[r];
-        u_ws[cl * DV + d] = (bf16)au[r];
+      for (int g4 = 0; g4 < 4; ++g4) {
+        bf16 pw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pw[e] = (bf16)(-aw[g4 * 4 + e]);
+        const int d = db * 32 + g4 * 8 + half * 4;
+        *reinterpret_cast<uint2*>(w_ws + l * DK + d) = *reinterpret_cast<uint2*>(pw);
       }
     }
   }
@@ -232,14 +303,31 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
 // ---------------------------------------------------------------------------
 // kernel 2: the sequential recurrence over chunks and the output
 // ---------------------------------------------------------------------------
+// Per-chunk operands of one thread, loaded one chunk ahead so that their
+// global-memory latency overlaps the current chunk's work.  Every wavefront
+// runs the same load sequence (only the base pointers differ), which keeps
+// the compiler's wait counts exact.
+struct ChunkOps {
+  bf16x8 a[DK / 16];  // waves 0, 1: rows of -w; waves 2, 3: rows of q
+  bf16x8 m[C / 16];   // waves 0, 1: rows of Tu; waves 2, 3: rows of Aqk
+  u32x4 kr[4];        // k rows 4vg..4vg+3, dims 8vc..8vc+7 (for the decayed k^T)
+  u32x4 vr;           // v row tid / 4, this slice's columns 8 (tid % 4) .. +7
+  float kdec[4];      // gc of those k rows
+  float gc;           // gc of token tid % C
+  float gc_last;
+};
+
 __global__ __launch_bounds__(256) void gdn_recur_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ h0,
-    const uint8_t* __restrict__ ws, bf16* __restrict__ o, float* __restrict__ hT, int B, int T,
-    int H, int NC, float scale) {
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ h0, const uint8_t* __restrict__ ws, bf16* __restrict__ o,
+    float* __restrict__ hT, int B, int T, int H, int NC, float scale) {
   constexpr int SP = DK + 8;  // row stride of S^T [v][d]
+  constexpr int OP = VS + 8;  // row stride of an output tile [token][v]
   __shared__ __attribute__((aligned(16))) bf16 st_s[VS * SP];      // bf16 S^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 wt_s[VS * CP];      // bf16 W^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 kd_s[2][DK * CP];   // (decayed k)^T
+  __shared__ __attribute__((aligned(16))) bf16 vt_s[2][VS * CP];   // v^T (slice)
+  __shared__ __attribute__((aligned(16))) bf16 ot_s[2][32 * OP];   // output tiles (waves 2, 3)
   __shared__ float gcb_s[2][C];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -254,6 +342,58 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
   const int h = bh % H, b = bh / H;
   const int v0 = vs * VS;
   const int64_t tok_stride = (int64_t)H * DK;
+  const int rblk = wave & 1;         // chunk rows 32*rblk .. 32*rblk+31 (A operands)
+  const int arow = rblk * 32 + col;  // A-operand row of this lane
+  const int vg = tid & 15, vc = tid >> 4;
+  const int vrow = tid >> 2, vcol = (tid & 3) * 8;
+
+  auto load = [&](int c, ChunkOps& op) {
+    const int t0 = c * C;
+    const int last = min(C, T - t0) - 1;  // rows past T read the last row (see below)
+    const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
+    const float* gc_ws = reinterpret_cast<const float*>(wsc + kGcOff);
+    // Rows past T are clamped onto the chunk's last row rather than zeroed:
+    // their q only reaches output rows that are not stored, and their k / v
+    // only meet rows and columns of W, Tu that are exactly zero (beta = 0).
+    const bf16* abase =
+        wave < 2 ? reinterpret_cast<const bf16*>(wsc + kWOff) + arow * DK
+                 : q + ((int64_t)b * T + t0 + min(arow, last)) * tok_stride + (int64_t)h * DK;
+    const bf16* mbase = reinterpret_cast<const bf16*>(wsc + (wave < 2 ? kTuOff : kAqkOff)) +
+                        arow * C;
+#pragma unroll
+    for (int ks = 0; ks < DK / 16; ++ks) op.a[ks] = ld8(abase + ks * 16 + half * 8);
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ++ks) op.m[ks] = ld8(mbase + ks * 16 + half * 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = min(4 * vg + i, last);
+      op.kr[i] = *reinterpret_cast<const u32x4*>(k + ((int64_t)b * T + t0 + row) * tok_stride +
+                                                 (int64_t)h * DK + vc * 8);
+      op.kdec[i] = gc_ws[4 * vg + i];
+    }
+    op.vr = *reinterpret_cast<const u32x4*>(
+        v + ((int64_t)b * T + t0 + min(vrow, last)) * tok_stride + (int64_t)h * DV + v0 + vcol);
+    op.gc = gc_ws[tid & (C - 1)];
+    op.gc_last = gc_ws[C - 1];
+  };
+  // (decayed k)^T, v^T and gc of a loaded chunk into LDS slot `buf`
+  auto stage = [&](const ChunkOps& op, int buf) {
+    u32x4 kr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float f = exp2f_fast((op.gc_last - op.kdec[i]) * kLog2e);
+      const bf16* e = reinterpret_cast<const bf16*>(&op.kr[i]);
+      bf16 sc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sc[j] = (bf16)((float)e[j] * f);
+      kr[i] = *reinterpret_cast<u32x4*>(sc);
+    }
+    store_transposed4x8(kd_s[buf], CP, vc * 8, 4 * vg, kr);
+    const bf16* ve = reinterpret_cast<const bf16*>(&op.vr);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) vt_s[buf][(vcol + j) * CP + vrow] = ve[j];
+    if (tid < C) gcb_s[buf][tid] = op.gc;
+  };
 
   // state rows of this wave: d = 32 * wave + (r / 4) * 8 + half * 4 + r % 4
   f32x16 s_acc;
@@ -272,82 +412,31 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
       *reinterpret_cast<uint2*>(st_s + col * SP + d) = *reinterpret_cast<uint2*>(p);
     }
   };
-  publish_state();
 
-  for (int c = 0; c < NC; ++c) {
+  // one chunk: `cur` holds its operands (staged: kd_s, vt_s, gcb_s [c & 1]);
+  // `nxt` receives chunk c + 1's
+  auto step = [&](int c, const ChunkOps& cur, ChunkOps& nxt) {
     const int buf = c & 1;
     const int t0 = c * C;
     const int n = min(C, T - t0);
-    const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
-    const bf16* w_ws = reinterpret_cast<const bf16*>(wsc + kWOff);
-    const bf16* u_ws = reinterpret_cast<const bf16*>(wsc + kUOff);
-    const bf16* aqk_ws = reinterpret_cast<const bf16*>(wsc + kAqkOff);
-    const float* gc_ws = reinterpret_cast<const float*>(wsc + kGcOff);
-    const float gc_last = gc_ws[C - 1];
+    if (c + 1 < NC) load(c + 1, nxt);
 
-    // (decayed k)^T for the state update: row l of k scaled by exp(gc_C - gc_l)
-    {
-      const int vg = tid & 15, vc = tid >> 4;
-      u32x4 kr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 4 * vg + i;
-        u32x4 raw = row < n ? *reinterpret_cast<const u32x4*>(
-                                  k + ((int64_t)b * T + t0 + row) * tok_stride +
-                                  (int64_t)h * DK + vc * 8)
-                            : u32x4{0, 0, 0, 0};
-        const float f = exp2f_fast((gc_last - gc_ws[row]) * kLog2e);
-        const bf16* e = reinterpret_cast<const bf16*>(&raw);
-        bf16 sc[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sc[j] = (bf16)((float)e[j] * f);
-        kr[i] = *reinterpret_cast<u32x4*>(sc);
-      }
-      store_transposed4x8(kd_s[buf], CP, vc * 8, 4 * vg, kr);
-    }
-    if (tid < C) gcb_s[buf][tid] = gc_ws[tid];
-
-    // operands from the workspace / q for this wave's 32 rows of the chunk
-    const int rblk = wave & 1;            // chunk rows 32*rblk .. 32*rblk+31
-    const int arow = rblk * 32 + col;     // A-operand row of this lane
-    bf16x8 areg[DK / 16];
-    float uval[16];
-    bf16x8 aqk[C / 16];
+    // waves 0, 1: W = Tu v - w S (rows 32 rblk ..); waves 2, 3: q S
+    f32x16 acc = {};
     if (wave < 2) {
 #pragma unroll
-      for (int ks = 0; ks < DK / 16; ++ks) areg[ks] = ld8(w_ws + arow * DK + ks * 16 + half * 8);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int cl = rblk * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        uval[r] = (float)u_ws[cl * DV + v0 + col];
-      }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < DK / 16; ++ks) {
-        bf16x8 a = {};
-        if (arow < n) {
-          u32x4 raw = *reinterpret_cast<const u32x4*>(
-              q + ((int64_t)b * T + t0 + arow) * tok_stride + (int64_t)h * DK + ks * 16 + half * 8);
-          a = *reinterpret_cast<bf16x8*>(&raw);
-        }
-        areg[ks] = a;
-      }
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ++ks) aqk[ks] = ld8(aqk_ws + arow * C + ks * 16 + half * 8);
+      for (int ks = 0; ks < C / 16; ++ks)
+        acc = mfma(cur.m[ks], ld8(vt_s[buf] + col * CP + ks * 16 + half * 8), acc);
     }
-    __syncthreads();  // (A) S^T, (decayed k)^T, gc of this chunk visible
-
-    // waves 0, 1: W = u - w S ; waves 2, 3: scale exp(gc) (q S)
-    f32x16 acc = {};
 #pragma unroll
     for (int ks = 0; ks < DK / 16; ++ks)
-      acc = mfma(areg[ks], ld8(st_s + col * SP + ks * 16 + half * 8), acc);
+      acc = mfma(cur.a[ks], ld8(st_s + col * SP + ks * 16 + half * 8), acc);
     if (wave < 2) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         bf16 p[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) p[e] = (bf16)(uval[g4 * 4 + e] - acc[g4 * 4 + e]);
+        for (int e = 0; e < 4; ++e) p[e] = (bf16)acc[g4 * 4 + e];
         const int cl = rblk * 32 + g4 * 8 + half * 4;
         *reinterpret_cast<uint2*>(wt_s + col * CP + cl) = *reinterpret_cast<uint2*>(p);
       }
@@ -358,29 +447,55 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
         acc[r] *= scale * exp2f_fast(gcb_s[buf][cl] * kLog2e);
       }
     }
-    __syncthreads();  // (B) W^T visible
+    __syncthreads();  // W^T visible
 
-    if (wave >= 2) {  // o = scale exp(gc) (q S) + Aqk W
+    bf16* ot = ot_s[wave & 1];
+    if (wave >= 2) {  // o = scale exp(gc) (q S) + Aqk W, into this wave's LDS tile
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks)
-        acc = mfma(aqk[ks], ld8(wt_s + col * CP + ks * 16 + half * 8), acc);
+        acc = mfma(cur.m[ks], ld8(wt_s + col * CP + ks * 16 + half * 8), acc);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int cl = rblk * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        if (cl < n) o[((int64_t)b * T + t0 + cl) * tok_stride + (int64_t)h * DV + v0 + col] =
-            (bf16)acc[r];
-      }
+      for (int r = 0; r < 16; ++r)
+        ot[((r >> 2) * 8 + half * 4 + (r & 3)) * OP + col] = (bf16)acc[r];
     }
     // S <- exp(gc_C) S + (decayed k)^T W   (rows 32 * wave .. of the state)
-    const float dec = exp2f_fast(gc_last * kLog2e);
+    const float dec = exp2f_fast(cur.gc_last * kLog2e);
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_acc[r] *= dec;
 #pragma unroll
     for (int ks = 0; ks < C / 16; ++ks)
       s_acc = mfma(ld8(kd_s[buf] + (32 * wave + col) * CP + ks * 16 + half * 8),
                    ld8(wt_s + col * CP + ks * 16 + half * 8), s_acc);
+    if (c + 1 < NC) stage(nxt, buf ^ 1);
     publish_state();
+    // output rows leave last, as 16-byte stores: nothing above waits on them
+    if (wave >= 2) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int rr = i * 16 + (lane >> 2), cc = (lane & 3) * 8;
+        const int cl = rblk * 32 + rr;
+        if (cl < n)
+          *reinterpret_cast<u32x4*>(o + ((int64_t)b * T + t0 + cl) * tok_stride +
+                                    (int64_t)h * DV + v0 + cc) =
+              *reinterpret_cast<const u32x4*>(ot + rr * OP + cc);
+      }
+    }
+    __syncthreads();  // next chunk's S^T, (decayed k)^T, v^T and gc visible
+  };
+
+  ChunkOps ops_a, ops_b;
+  if (NC > 0) {
+    load(0, ops_a);
+    stage(ops_a, 0);
   }
+  publish_state();
+  __syncthreads();
+  int c = 0;
+  for (; c + 1 < NC; c += 2) {
+    step(c, ops_a, ops_b);
+    step(c + 1, ops_b, ops_a);
+  }
+  if (c < NC) step(c, ops_a, ops_b);
 
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -427,10 +542,9 @@ extern "C" int tileops_gdn_prefill_fwd(const void* q, const void* k, const void*
   const bf16* kb = static_cast<const bf16*>(k);
   if (nblk > 0)
     gdn::gdn_prep_kernel<<<dim3((unsigned)nblk), dim3(256), 0, s>>>(
-        qb, kb, static_cast<const bf16*>(v), g, beta, static_cast<uint8_t*>(ws), (int)B, (int)T,
-        (int)H, nc, scale);
+        qb, kb, g, beta, static_cast<uint8_t*>(ws), (int)B, (int)T, (int)H, nc, scale);
   gdn::gdn_recur_kernel<<<dim3((unsigned)(B * H * (gdn::DV / gdn::VS))), dim3(256), 0, s>>>(
-      qb, kb, h0, static_cast<const uint8_t*>(ws), static_cast<bf16*>(o), hT, (int)B, (int)T,
-      (int)H, nc, scale);
+      qb, kb, static_cast<const bf16*>(v), h0, static_cast<const uint8_t*>(ws),
+      static_cast<bf16*>(o), hT, (int)B, (int)T, (int)H, nc, scale);
   return launch_status();
 }
