@@ -49,6 +49,24 @@ def test_fused_add_layer_norm_op(m, n, dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("param_dtype", [None, torch.float32])
+def test_fused_add_layer_norm_many_rows(param_dtype):
+    # more rows than the device holds resident workgroups (the persistent
+    # path), and a row count that is not a multiple of the rows per
+    # workgroup: residual_out bit-exact on every row, y on sampled rows
+    m, n, dtype = 12289, 4096, torch.bfloat16
+    test = FusedAddLayerNormTest(m, n, dtype, param_dtype=param_dtype)
+    x, r, w, b = test.gen_inputs()
+    y, r_out = FusedAddLayerNormFwdOp(dtype=dtype)(x, r, w, b)
+    assert torch.equal(r_out, (x.float() + r.float()).to(dtype))
+    rows = torch.arange(0, m, 97, device=x.device)
+    rows = torch.cat([rows, torch.tensor([m - 1], device=x.device)])
+    y_ref, _ = test.ref_program(x[rows], r[rows], w, b)
+    atol, rtol = ref_tolerance(dtype)
+    torch.testing.assert_close(y[rows], y_ref.to(y.device), atol=atol, rtol=rtol)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_fused_add_layer_norm_fp32_params(dtype):
     test = FusedAddLayerNormTest(256, 4096, dtype, param_dtype=torch.float32)

@@ -22,7 +22,9 @@ from tileops.device import get_device_backend  # noqa: E402
 
 
 def pytest_collect_file(file_path, parent):
-    if file_path.suffix == ".py" and file_path.name.startswith("bench_"):
+    # files named on the command line are collected by pytest itself
+    if (file_path.suffix == ".py" and file_path.name.startswith("bench_")
+            and not parent.session.isinitpath(file_path)):
         return pytest.Module.from_parent(parent, path=file_path)
     return None
 

@@ -20,6 +20,34 @@ __device__ __forceinline__ float wload(const W* p, int64_t i) {
   return Elem<W>::to_f32(p[i]);
 }
 
+// w / b into LDS as fp32 by the whole workgroup (NT threads); 16-byte loads
+// when the host found both 16-byte aligned and N a multiple of the pack.
+template <typename W, int NT>
+__device__ __forceinline__ void stage_params(float* sw, float* sb, const W* w, const W* b, int N,
+                                             bool vec) {
+  constexpr int PV = 16 / sizeof(W);  // parameters per 16-byte load
+  if (vec) {
+    for (int i = threadIdx.x; i < N / PV; i += NT) {
+      const Pack<W> pw = *reinterpret_cast<const Pack<W>*>(w + (int64_t)i * PV);
+      const Pack<W> pb = *reinterpret_cast<const Pack<W>*>(b + (int64_t)i * PV);
+#pragma unroll
+      for (int e = 0; e < PV; e += 4) {
+        *reinterpret_cast<float4*>(sw + i * PV + e) =
+            make_float4(Elem<W>::to_f32(pw.v[e]), Elem<W>::to_f32(pw.v[e + 1]),
+                        Elem<W>::to_f32(pw.v[e + 2]), Elem<W>::to_f32(pw.v[e + 3]));
+        *reinterpret_cast<float4*>(sb + i * PV + e) =
+            make_float4(Elem<W>::to_f32(pb.v[e]), Elem<W>::to_f32(pb.v[e + 1]),
+                        Elem<W>::to_f32(pb.v[e + 2]), Elem<W>::to_f32(pb.v[e + 3]));
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < N; i += NT) {
+      sw[i] = wload(w, i);
+      sb[i] = wload(b, i);
+    }
+  }
+}
+
 // One wavefront per row, WPB rows per workgroup (one-shot grid).  The
 // workgroup stages w / b into LDS (fp32), then each lane loads its KP packs
 // of x and residual; the rounded sum stays in registers in the storage type
@@ -28,7 +56,7 @@ template <typename T, typename W, int KP, int WPB>
 __global__ __launch_bounds__(WPB * 64) void fused_add_ln_wave_kernel(
     const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
     const W* __restrict__ b, T* __restrict__ y, T* __restrict__ rout, int64_t M, int N,
-    float eps) {
+    float eps, bool vec_params) {
   constexpr int V = Elem<T>::kVec;
   extern __shared__ float smem[];  // w[N] then b[N], fp32
   float* sw = smem;
@@ -40,10 +68,7 @@ __global__ __launch_bounds__(WPB * 64) void fused_add_ln_wave_kernel(
   const T* xr = x + row * N;
   const T* rr = res + row * N;
 
-  for (int i = threadIdx.x; i < N; i += WPB * 64) {
-    sw[i] = wload(w, i);
-    sb[i] = wload(b, i);
-  }
+  stage_params<W, WPB * 64>(sw, sb, w, b, N, vec_params);
   __syncthreads();
   if (!live) return;
   Pack<T> xs[KP], rs[KP];
@@ -153,8 +178,9 @@ static void launch_wave(const T* x, const T* r, const W* w, const W* b, T* y, T*
   constexpr int WPB = 4;
   const size_t lds = (size_t)N * 2 * sizeof(float);
   const int64_t blocks = (M + WPB - 1) / WPB;
+  const bool vec = N % (16 / (int)sizeof(W)) == 0 && host_aligned16(w) && host_aligned16(b);
   fused_add_ln_wave_kernel<T, W, KP, WPB><<<dim3((unsigned)blocks), dim3(WPB * 64), lds, s>>>(
-      x, r, w, b, y, ro, M, N, eps);
+      x, r, w, b, y, ro, M, N, eps, vec);
 }
 
 template <typename T, typename W>
