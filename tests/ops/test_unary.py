@@ -98,6 +98,18 @@ def test_clamp_scalar_param_forms(min_val, max_val):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_activations_all_half_encodings_bitexact(dtype):
+    """Every one of the 65,536 encodings (NaN, ±inf, ±0, subnormals included)
+    through hardswish and hardsigmoid, bit for bit against the oracle."""
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(dtype).cuda()
+    for op_cls, fn in ((HardswishFwdOp, orc.hardswish), (HardsigmoidFwdOp, orc.hardsigmoid)):
+        got = to_np(op_cls(N_total=x.numel(), dtype=dtype)(x))
+        assert_bits_equal(got, fn(to_np(x), NAMES[dtype]), f"{op_cls.__name__} {dtype}")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_unary_special_values_bitexact(dtype):
     """Boundary cases of the reference harness (hardswish_fwd_kernel.py:267-337):

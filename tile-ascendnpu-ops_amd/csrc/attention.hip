@@ -1,8 +1,9 @@
 // Flash-attention forward for gfx950 (tileops_mha_fwd), BSHD layout.
 //
-// One workgroup = 4 wavefronts = BM = 128 query rows of one (batch, head);
-// each wavefront owns 32 query rows.  Keys/values stream through LDS in
-// tiles of BN = 64 rows, prefetched into registers one tile ahead.
+// One workgroup = WAVES wavefronts (8 at launch: BM = 256 query rows of one
+// (batch, head)); each wavefront owns 32 query rows.  Keys/values stream
+// through LDS in tiles of BN = 64 rows, prefetched into registers one tile
+// ahead.
 //
 // Both products run on v_mfma_f32_32x32x16_{bf16,f16} in the *transposed*
 // orientation:

@@ -16,6 +16,20 @@ namespace tileops {
 // gives torch's NaN propagation without a separate isnan test; fmaxf/fminf
 // are avoided because they drop NaN.
 // ---------------------------------------------------------------------------
+// n / 6 correctly rounded without the IEEE division sequence: q0 = n * RN(1/6)
+// is within one ulp, the remainder e = n - 6 q0 is exact under FMA, and
+// RN(q0 + e RN(1/6)) is then the correctly rounded quotient (Markstein's
+// one-step correction; 6 is not of the form 2^k (2 - 2^-23)).  Exact
+// quotients (e == 0, which keeps the sign of zero) and non-finite values
+// keep q0.
+__device__ __forceinline__ float div6(float n) {
+  const float r = 0x1.555556p-3f;  // RN(1/6)
+  const float q0 = n * r;
+  const float e = fmaf(-q0, 6.0f, n);
+  const float q1 = fmaf(e, r, q0);
+  return (e == 0.0f || !(__builtin_fabsf(q0) < __builtin_huge_valf())) ? q0 : q1;
+}
+
 template <int OP>
 __device__ __forceinline__ float unary_op(float x, float lo, float hi, int flags) {
   if constexpr (OP == TILEOPS_HARDSWISH) {
@@ -23,13 +37,13 @@ __device__ __forceinline__ float unary_op(float x, float lo, float hi, int flags
     float t = x + 3.0f;
     t = t < 0.0f ? 0.0f : t;
     t = t > 6.0f ? 6.0f : t;
-    return x * t / 6.0f;
+    return div6(x * t);
   } else if constexpr (OP == TILEOPS_HARDSIGMOID) {
     // min(max(x + 3, 0), 6) / 6  (F.hardsigmoid; test_hardsigmoid.py:38-39)
     float t = x + 3.0f;
     t = t < 0.0f ? 0.0f : t;
     t = t > 6.0f ? 6.0f : t;
-    return t / 6.0f;
+    return div6(t);
   } else {
     // torch.clamp(x, min, max) (test_clamp_scalar.py:56-57): NaN input stays
     // NaN; a NaN bound selects the bound itself, i.e. NaN everywhere; with
@@ -134,32 +148,45 @@ __device__ __forceinline__ uint32_t pred_bit(typename FpBits<T>::U b) {
   else return (b & F::kExp) != F::kExp ? 1u : 0u;
 }
 
-// One input pack per thread (one-shot grid): 4 fp32 or 8 half inputs give a
-// 4- or 8-byte store of 0/1 bytes.
+// Two input packs per thread, 256 packs apart inside the workgroup's span
+// (measured on MI355X: 85% of HBM peak at fp32 8192^2, against 76% with one
+// pack per thread); 4 fp32 or 8 half inputs give a 4- or 8-byte store of 0/1
+// bytes.
 template <typename T> struct PredOut;
 template <> struct PredOut<float> { typedef uint32_t W; };
 template <> struct PredOut<f16> { typedef uint2 W; };
 template <> struct PredOut<bf16> { typedef uint2 W; };
+constexpr int kIsfpPacks = 2;
 
 template <typename T, int PRED>
 __global__ __launch_bounds__(256) void isfp_vec_kernel(const T* __restrict__ x,
                                                        uint8_t* __restrict__ y, int64_t npack) {
   typedef typename FpBits<T>::U U;
   constexpr int V = Elem<T>::kVec;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= npack) return;
-  const u32x4 in = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + i * V));
-  const U* e = reinterpret_cast<const U*>(&in);
-  uint32_t words[V / 4];
+  const int64_t base = (int64_t)blockIdx.x * 256 * kIsfpPacks + threadIdx.x;
+  u32x4 in[kIsfpPacks];
 #pragma unroll
-  for (int w = 0; w < V / 4; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) word |= pred_bit<T, PRED>(e[w * 4 + b]) << (8 * b);
-    words[w] = word;
+  for (int u = 0; u < kIsfpPacks; ++u) {
+    const int64_t i = base + (int64_t)u * 256;
+    if (i < npack) in[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + i * V));
   }
-  *reinterpret_cast<typename PredOut<T>::W*>(y + i * V) =
-      *reinterpret_cast<typename PredOut<T>::W*>(words);
+#pragma unroll
+  for (int u = 0; u < kIsfpPacks; ++u) {
+    const int64_t i = base + (int64_t)u * 256;
+    if (i < npack) {
+      const U* e = reinterpret_cast<const U*>(&in[u]);
+      uint32_t words[V / 4];
+#pragma unroll
+      for (int w = 0; w < V / 4; ++w) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) word |= pred_bit<T, PRED>(e[w * 4 + b]) << (8 * b);
+        words[w] = word;
+      }
+      *reinterpret_cast<typename PredOut<T>::W*>(y + i * V) =
+          *reinterpret_cast<typename PredOut<T>::W*>(words);
+    }
+  }
 }
 
 template <typename T, int PRED>
@@ -179,7 +206,7 @@ static int launch_isfp(const void* xv, uint8_t* y, int64_t n, hipStream_t s) {
   const bool aligned = host_aligned16(x) && (reinterpret_cast<uintptr_t>(y) % V) == 0;
   const int64_t npack = aligned ? n / V : 0;
   if (npack > 0) {
-    const int64_t grid = (npack + 255) / 256;
+    const int64_t grid = (npack + 256 * kIsfpPacks - 1) / (256 * kIsfpPacks);
     isfp_vec_kernel<T, PRED><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, y, npack);
   }
   int64_t done = npack * V;
