@@ -20,25 +20,59 @@ __device__ __forceinline__ float wload(const W* p, int64_t i) {
   return Elem<W>::to_f32(p[i]);
 }
 
-// w / b into LDS as fp32 by the whole workgroup (NT threads); 16-byte loads
-// when the host found both 16-byte aligned and N a multiple of the pack.
+// w / b into LDS as fp32 by the whole workgroup (NT threads).  With 16-byte
+// loads (vec: both 16-byte aligned, N a multiple of the pack) the first
+// SB * NT packs of each come from one batch of loads issued by stage_fetch
+// before the caller's row loads, so that their wait in stage_store does not
+// also wait for the row data behind them; longer rows finish in a loop.
+template <typename W>
+struct ParamBatch {
+  static constexpr int SB = 4;
+  Pack<W> w[SB], b[SB];
+};
+
 template <typename W, int NT>
-__device__ __forceinline__ void stage_params(float* sw, float* sb, const W* w, const W* b, int N,
-                                             bool vec) {
-  constexpr int PV = 16 / sizeof(W);  // parameters per 16-byte load
-  if (vec) {
-    for (int i = threadIdx.x; i < N / PV; i += NT) {
-      const Pack<W> pw = *reinterpret_cast<const Pack<W>*>(w + (int64_t)i * PV);
-      const Pack<W> pb = *reinterpret_cast<const Pack<W>*>(b + (int64_t)i * PV);
+__device__ __forceinline__ void stage_fetch(ParamBatch<W>& pb, const W* w, const W* b, int N,
+                                            bool vec) {
+  constexpr int PV = 16 / sizeof(W);
+  if (!vec) return;
+  const int nv = N / PV;
 #pragma unroll
-      for (int e = 0; e < PV; e += 4) {
-        *reinterpret_cast<float4*>(sw + i * PV + e) =
-            make_float4(Elem<W>::to_f32(pw.v[e]), Elem<W>::to_f32(pw.v[e + 1]),
-                        Elem<W>::to_f32(pw.v[e + 2]), Elem<W>::to_f32(pw.v[e + 3]));
-        *reinterpret_cast<float4*>(sb + i * PV + e) =
-            make_float4(Elem<W>::to_f32(pb.v[e]), Elem<W>::to_f32(pb.v[e + 1]),
-                        Elem<W>::to_f32(pb.v[e + 2]), Elem<W>::to_f32(pb.v[e + 3]));
+  for (int j = 0; j < ParamBatch<W>::SB; ++j) {
+    const int i = min((int)threadIdx.x + j * NT, nv - 1);
+    pb.w[j] = *reinterpret_cast<const Pack<W>*>(w + (int64_t)i * PV);
+    pb.b[j] = *reinterpret_cast<const Pack<W>*>(b + (int64_t)i * PV);
+  }
+}
+
+template <typename W>
+__device__ __forceinline__ void put_pack(float* dst, const Pack<W>& p) {
+  constexpr int PV = 16 / sizeof(W);
+#pragma unroll
+  for (int e = 0; e < PV; e += 4)
+    *reinterpret_cast<float4*>(dst + e) =
+        make_float4(Elem<W>::to_f32(p.v[e]), Elem<W>::to_f32(p.v[e + 1]),
+                    Elem<W>::to_f32(p.v[e + 2]), Elem<W>::to_f32(p.v[e + 3]));
+}
+
+template <typename W, int NT>
+__device__ __forceinline__ void stage_store(const ParamBatch<W>& pb, float* sw, float* sb,
+                                            const W* w, const W* b, int N, bool vec) {
+  constexpr int PV = 16 / sizeof(W);
+  constexpr int SB = ParamBatch<W>::SB;
+  if (vec) {
+    const int nv = N / PV;
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int i = threadIdx.x + j * NT;
+      if (i < nv) {
+        put_pack<W>(sw + i * PV, pb.w[j]);
+        put_pack<W>(sb + i * PV, pb.b[j]);
       }
+    }
+    for (int i = threadIdx.x + SB * NT; i < nv; i += NT) {
+      put_pack<W>(sw + i * PV, *reinterpret_cast<const Pack<W>*>(w + (int64_t)i * PV));
+      put_pack<W>(sb + i * PV, *reinterpret_cast<const Pack<W>*>(b + (int64_t)i * PV));
     }
   } else {
     for (int i = threadIdx.x; i < N; i += NT) {
@@ -65,33 +99,39 @@ __global__ __launch_bounds__(WPB * 64) void fused_add_ln_wave_kernel(
   const int npack = N / V;
   const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
   const bool live = row < M;
-  const T* xr = x + row * N;
-  const T* rr = res + row * N;
 
-  stage_params<W, WPB * 64>(sw, sb, w, b, N, vec_params);
-  __syncthreads();
-  if (!live) return;
+  // Parameter loads, then the row loads, then the parameters into LDS: the
+  // two streams overlap.  Every lane loads all KP packs, past-the-end ones
+  // clamped onto the row's last pack, so the loads are one uniform sequence
+  // the compiler can wait on one at a time; lanes mask those packs out of
+  // the sums and the stores.
+  ParamBatch<W> pb;
+  stage_fetch<W, WPB * 64>(pb, w, b, N, vec_params);
   Pack<T> xs[KP], rs[KP];
+  const int64_t rowc = live ? row : M - 1;  // dead waves load a live row
 #pragma unroll
   for (int k = 0; k < KP; ++k) {
-    const int p = k * 64 + lane;
-    if (p < npack) {
-      xs[k] = load_pack_nt(xr + (int64_t)p * V);
-      rs[k] = load_pack_nt(rr + (int64_t)p * V);
-    }
+    const int p = min(k * 64 + lane, npack - 1);
+    xs[k] = load_pack_nt(x + rowc * N + (int64_t)p * V);
+    rs[k] = load_pack_nt(res + rowc * N + (int64_t)p * V);
   }
+  stage_store<W, WPB * 64>(pb, sw, sb, w, b, N, vec_params);
+  __syncthreads();
+  if (!live) return;
 
   float sum = 0.0f;
 #pragma unroll
   for (int k = 0; k < KP; ++k) {
     const int p = k * 64 + lane;
-    if (p < npack) {
+    float part = 0.0f;
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        const T s = Elem<T>::from_f32(Elem<T>::to_f32(xs[k].v[e]) + Elem<T>::to_f32(rs[k].v[e]));
-        xs[k].v[e] = s;
-        sum += Elem<T>::to_f32(s);
-      }
+    for (int e = 0; e < V; ++e) {
+      const T s = Elem<T>::from_f32(Elem<T>::to_f32(xs[k].v[e]) + Elem<T>::to_f32(rs[k].v[e]));
+      xs[k].v[e] = s;
+      part += Elem<T>::to_f32(s);
+    }
+    if (p < npack) {
+      sum += part;
       store_pack_nt(rout + row * N + (int64_t)p * V, xs[k]);
     }
   }
@@ -100,27 +140,34 @@ __global__ __launch_bounds__(WPB * 64) void fused_add_ln_wave_kernel(
   float sq = 0.0f;
 #pragma unroll
   for (int k = 0; k < KP; ++k) {
-    const int p = k * 64 + lane;
-    if (p < npack) {
+    float part = 0.0f;
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
-        sq = fmaf(d, d, sq);
-      }
+    for (int e = 0; e < V; ++e) {
+      const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
+      part = fmaf(d, d, part);
     }
+    if (k * 64 + lane < npack) sq += part;
   }
   const float rstd = 1.0f / sqrtf(wave_sum(sq) * inv_n + eps);
 #pragma unroll
   for (int k = 0; k < KP; ++k) {
     const int p = k * 64 + lane;
     if (p < npack) {
+      // N is a multiple of the pack (>= 4 elements) on this path, so both
+      // parameter rows and every lane's slice of them are 16-byte aligned
+      float wv[V], bv[V];
+#pragma unroll
+      for (int e = 0; e < V; e += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(sw + p * V + e);
+        const float4 b4 = *reinterpret_cast<const float4*>(sb + p * V + e);
+        wv[e] = w4.x; wv[e + 1] = w4.y; wv[e + 2] = w4.z; wv[e + 3] = w4.w;
+        bv[e] = b4.x; bv[e + 1] = b4.y; bv[e + 2] = b4.z; bv[e + 3] = b4.w;
+      }
       Pack<T> o;
-      const float* wp = sw + p * V;
-      const float* bp = sb + p * V;
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
-        o.v[e] = Elem<T>::from_f32(fmaf(d * rstd, wp[e], bp[e]));
+        o.v[e] = Elem<T>::from_f32(fmaf(d * rstd, wv[e], bv[e]));
       }
       store_pack_nt(y + row * N + (int64_t)p * V, o);
     }
