@@ -16,10 +16,12 @@
 // Only differences gc_l - gc_s <= 0, gc_C - gc_l <= 0 and gc <= 0 are ever
 // exponentiated, so nothing overflows however strong the decay.
 //
-// Kernel 1 (one workgroup per chunk, two per CU): K K^T and Q K^T on bf16
-// MFMA, the 64x64 unit-lower-triangular inverse in fp32 (32x32 diagonal
-// blocks by substitution, the off-diagonal block by two small products),
-// then w on MFMA.  -w, Tu, Aqk and gc go to a workspace.
+// Kernel 1 (persistent, two workgroups per CU, the next chunk's q / k / g /
+// beta loaded while the current one is processed): K K^T and Q K^T on bf16
+// MFMA, the 64x64 unit-lower-triangular inverse in fp32 (16x16 diagonal
+// blocks by substitution, one wavefront each, the off-diagonal blocks by
+// products on fp32 MFMA), then w on bf16 MFMA.  -w, Tu, Aqk and gc go to a
+// workspace.
 // Kernel 2 (one workgroup per (b, h, 32-wide slice of V), 4 wavefronts):
 // the state slice lives in MFMA accumulators (wavefront i owns key rows
 // 32i..32i+31), its bf16 copy and W are exchanged through LDS.  Every
@@ -87,6 +89,17 @@ __device__ __forceinline__ void store_transposed4x8(bf16* dst, int stride, int d
 constexpr int AS = 72;  // fp32 row stride of A^T / T (288 bytes: float4-aligned rows)
 constexpr int XS = 36;  // fp32 row stride of X
 
+// Global operands of one chunk for one thread, loaded a chunk ahead: k rows
+// 4vg..4vg+3 (dims 8vc..8vc+7), g / beta of token `lane`, and the q row this
+// wavefront's Q K^T block needs, in the MFMA A layout.  One uniform sequence
+// for every wavefront (wave 3 loads q rows it does not use); rows past T load
+// the chunk's last row and are zeroed where they are consumed.
+struct PrepLoads {
+  u32x4 kr[4];
+  bf16x8 aq[DK / 16];
+  float g, beta;
+};
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ g,
     const float* __restrict__ beta, uint8_t* __restrict__ ws, int B, int T, int H, int NC,
@@ -96,7 +109,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(16))) float x_s[32 * XS];
   __shared__ __attribute__((aligned(16))) bf16 kT_s[DK * CP];
   __shared__ __attribute__((aligned(16))) bf16 aqk_s[C * CP];
-  __shared__ float gc_s[C], beta_s[C], be_s[C];
+  __shared__ __attribute__((aligned(16))) float gc_s[C], beta_s[C], be_s[C];
   static_assert(C * KP * 2 <= C * AS * 4, "k tile must fit the T region");
   static_assert(2 * C * CP * 2 <= C * AS * 4, "Tw and Tu must fit the A region");
   bf16* k_s = reinterpret_cast<bf16*>(r0);
@@ -107,196 +120,255 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
-  const int chunk = blockIdx.x % NC;
-  const int bh = blockIdx.x / NC;
-  const int h = bh % H, b = bh / H;
-  const int t0 = chunk * C;
-  const int n = min(C, T - t0);
+  const int rb = wave == 0 ? 0 : 1;  // Q K^T / K K^T block of waves 0-2
+  const int cb = wave == 2 ? 1 : 0;
+  const int qrow = rb * 32 + col;
+  const int vg = tid & 15, vc = tid >> 4;
   const int64_t tok_stride = (int64_t)H * DK;  // DK == DV
-  uint8_t* wsc = ws + (size_t)blockIdx.x * kChunkBytes;
-  bf16* w_ws = reinterpret_cast<bf16*>(wsc + kWOff);
-  bf16* tu_ws = reinterpret_cast<bf16*>(wsc + kTuOff);
-  bf16* aqk_ws = reinterpret_cast<bf16*>(wsc + kAqkOff);
-  float* gc_ws = reinterpret_cast<float*>(wsc + kGcOff);
+  const uint64_t nblk = (uint64_t)B * H * NC;
 
-  // ---- stage k (natural + transposed); rows past T are 0
-  {
-    const int vg = tid & 15, vc = tid >> 4;  // rows 4vg..4vg+3, dims 8vc..8vc+7
-    u32x4 kr[4];
+  auto load = [&](uint64_t blk, PrepLoads& L) {
+    const int chunk = (int)(blk % NC), bh = (int)(blk / NC);
+    const int h = bh % H, b = bh / H;
+    const int t0 = chunk * C, n = min(C, T - t0);
+    const bf16* kb = k + ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK + vc * 8;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * vg + i;
-      const int64_t off = ((int64_t)b * T + t0 + row) * tok_stride + (int64_t)h * DK + vc * 8;
-      kr[i] = row < n ? *reinterpret_cast<const u32x4*>(k + off) : u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(k_s + row * KP + vc * 8) = kr[i];
-    }
-    store_transposed4x8(kT_s, CP, vc * 8, 4 * vg, kr);
-  }
-  if (wave == 0) {
-    const int64_t gi = ((int64_t)b * T + t0 + lane) * H + h;
-    float x = lane < n ? g[gi] : 0.0f;
-    const float bt = lane < n ? beta[gi] : 0.0f;
+    for (int i = 0; i < 4; ++i)
+      L.kr[i] = *reinterpret_cast<const u32x4*>(kb + min(4 * vg + i, n - 1) * tok_stride);
+    const int64_t gi = ((int64_t)b * T + t0 + min(lane, n - 1)) * H + h;
+    L.g = g[gi];
+    L.beta = beta[gi];
+    const bf16* qp = q + ((int64_t)b * T + t0 + min(qrow, n - 1)) * tok_stride + (int64_t)h * DK;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {  // inclusive prefix sum over the chunk
-      const float y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
-    gc_s[lane] = x;
-    beta_s[lane] = bt;
-    be_s[lane] = bt * exp2f_fast(x * kLog2e);
-    gc_ws[lane] = x;
-  }
-  __syncthreads();
+    for (int ks = 0; ks < DK / 16; ++ks) L.aq[ks] = ld8(qp + ks * 16 + half * 8);
+  };
 
-  // ---- K K^T -> A^T (fp32, LDS) and Q K^T -> Aqk (bf16, LDS), in 32x32
-  // blocks (row block rb, column block cb).  Only the strictly lower parts of
-  // the diagonal blocks and the block A21 of A are ever read back.
-  if (wave < 3) {
-    const int rb = wave == 0 ? 0 : 1;
-    const int cb = wave == 2 ? 1 : 0;
-    const int qrow = rb * 32 + col;
-    f32x16 kk = {}, qk = {};
+  // Persistent: workgroup i takes chunks i, i + grid, ...; the next chunk's
+  // loads are issued as soon as the current one's registers are consumed.
+  PrepLoads cur;
+  uint64_t blk = blockIdx.x;
+  if (blk < nblk) load(blk, cur);
+  for (; blk < nblk; blk += gridDim.x) {
+    const int chunk = (int)(blk % NC);
+    const int t0 = chunk * C;
+    const int n = min(C, T - t0);
+    uint8_t* wsc = ws + (size_t)blk * kChunkBytes;
+    bf16* w_ws = reinterpret_cast<bf16*>(wsc + kWOff);
+    bf16* tu_ws = reinterpret_cast<bf16*>(wsc + kTuOff);
+    bf16* aqk_ws = reinterpret_cast<bf16*>(wsc + kAqkOff);
+    float* gc_ws = reinterpret_cast<float*>(wsc + kGcOff);
+    u32x4 (&kr)[4] = cur.kr;
+
+    // ---- stage k (natural + transposed); rows past T are 0
+    {
 #pragma unroll
-    for (int ks = 0; ks < DK / 16; ++ks) {
-      const bf16x8 bk = ld8(k_s + (cb * 32 + col) * KP + ks * 16 + half * 8);
-      const bf16x8 ak = ld8(k_s + (rb * 32 + col) * KP + ks * 16 + half * 8);
-      bf16x8 aq = {};
-      if (qrow < n) {
-        u32x4 raw = *reinterpret_cast<const u32x4*>(
-            q + ((int64_t)b * T + t0 + qrow) * tok_stride + (int64_t)h * DK + ks * 16 + half * 8);
-        aq = *reinterpret_cast<bf16x8*>(&raw);
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * vg + i;
+        if (row >= n) kr[i] = u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(k_s + row * KP + vc * 8) = kr[i];
       }
-      kk = mfma(ak, bk, kk);
-      qk = mfma(aq, bk, qk);
+      store_transposed4x8(kT_s, CP, vc * 8, 4 * vg, kr);
     }
-    const int cs = cb * 32 + col;
-    const float gcs = gc_s[cs];
+    if (wave == 0) {
+      float x = lane < n ? cur.g : 0.0f;
+      const float bt = lane < n ? cur.beta : 0.0f;
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      float a4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = g4 * 4 + e;
-        const int cl = rb * 32 + g4 * 8 + half * 4 + e;
-        const float gd = cl >= cs ? exp2f_fast((gc_s[cl] - gcs) * kLog2e) : 0.0f;
-        a4[e] = cl > cs ? beta_s[cl] * gd * kk[r] : 0.0f;
-        aqk_s[cl * CP + cs] = (bf16)(scale * gd * qk[r]);
+      for (int o = 1; o < 64; o <<= 1) {  // inclusive prefix sum over the chunk
+        const float y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
       }
-      const int cl0 = rb * 32 + g4 * 8 + half * 4;
-      *reinterpret_cast<float4*>(at_s + cs * AS + cl0) = make_float4(a4[0], a4[1], a4[2], a4[3]);
+      gc_s[lane] = x;
+      beta_s[lane] = bt;
+      be_s[lane] = bt * exp2f_fast(x * kLog2e);
+      gc_ws[lane] = x;
     }
-  } else {
-    const int cs = 32 + col;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) aqk_s[((r >> 2) * 8 + half * 4 + (r & 3)) * CP + cs] = (bf16)0.0f;
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // ---- Aqk rows to the workspace (16-byte stores); T = (I + A)^-1, blocked:
-  // T11 = (I + A11)^-1 and T22 = (I + A22)^-1 by right-looking substitution
-  // (wave 0: lanes 0-31 own the columns of T11, lanes 32-63 those of T22;
-  // p[i] accumulates sum_m A[i][m] T[m][j]), then T21 = -T22 (A21 T11).
+    // ---- K K^T -> A^T (fp32, LDS) and Q K^T -> Aqk (bf16, LDS), in 32x32
+    // blocks (row block rb, column block cb).  Only the strictly lower parts of
+    // the diagonal blocks and the block A21 of A are ever read back.
+    if (wave < 3) {
+      f32x16 kk = {}, qk = {};
+      const bool qlive = qrow < n;
 #pragma unroll
-  for (int e = tid; e < C * C / 8; e += 256) {
-    const int row = e >> 3, c8 = (e & 7) * 8;
-    *reinterpret_cast<u32x4*>(aqk_ws + row * C + c8) =
-        *reinterpret_cast<const u32x4*>(aqk_s + row * CP + c8);
-  }
-  if (wave == 0) {
-    const int base = half * 32, jl = col;
-    float p[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) p[i] = 0.0f;
-#pragma unroll
-    for (int m = 0; m < 32; ++m) {
-      const float t = (m == jl ? 1.0f : 0.0f) - p[m];
-      t_s[(base + m) * AS + base + jl] = t;
-      const float* acol = at_s + (base + m) * AS + base;  // A[base + i][base + m], i = 0..31
-#pragma unroll
-      for (int i4 = ((m + 1) >> 2) << 2; i4 < 32; i4 += 4) {
-        const float4 a4 = *reinterpret_cast<const float4*>(acol + i4);
-        if (i4 + 0 > m) p[i4 + 0] = fmaf(a4.x, t, p[i4 + 0]);
-        if (i4 + 1 > m) p[i4 + 1] = fmaf(a4.y, t, p[i4 + 1]);
-        if (i4 + 2 > m) p[i4 + 2] = fmaf(a4.z, t, p[i4 + 2]);
-        if (i4 + 3 > m) p[i4 + 3] = fmaf(a4.w, t, p[i4 + 3]);
+      for (int ks = 0; ks < DK / 16; ++ks) {
+        const bf16x8 bk = ld8(k_s + (cb * 32 + col) * KP + ks * 16 + half * 8);
+        const bf16x8 ak = ld8(k_s + (rb * 32 + col) * KP + ks * 16 + half * 8);
+        const bf16x8 a = qlive ? cur.aq[ks] : bf16x8{};
+        kk = mfma(ak, bk, kk);
+        qk = mfma(a, bk, qk);
       }
-    }
-  }
-  __syncthreads();
-  const int xj = tid & 31, xi = (tid >> 5) * 4;  // this thread: rows xi..xi+3, column xj
-  {
-    float x0 = 0.0f, x1 = 0.0f, x2 = 0.0f, x3 = 0.0f;  // X = A21 T11
-#pragma unroll 8
-    for (int kx = 0; kx < 32; ++kx) {
-      const float4 a4 = *reinterpret_cast<const float4*>(at_s + kx * AS + 32 + xi);
-      const float tk = t_s[kx * AS + xj];
-      x0 = fmaf(a4.x, tk, x0);
-      x1 = fmaf(a4.y, tk, x1);
-      x2 = fmaf(a4.z, tk, x2);
-      x3 = fmaf(a4.w, tk, x3);
-    }
-    x_s[(xi + 0) * XS + xj] = x0;
-    x_s[(xi + 1) * XS + xj] = x1;
-    x_s[(xi + 2) * XS + xj] = x2;
-    x_s[(xi + 3) * XS + xj] = x3;
-  }
-  __syncthreads();
-  {
-    float y0 = 0.0f, y1 = 0.0f, y2 = 0.0f, y3 = 0.0f;  // T21 = -T22 X
-#pragma unroll 8
-    for (int kx = 0; kx < 32; ++kx) {
-      const float xk = x_s[kx * XS + xj];
-      y0 = fmaf(t_s[(32 + xi + 0) * AS + 32 + kx], xk, y0);
-      y1 = fmaf(t_s[(32 + xi + 1) * AS + 32 + kx], xk, y1);
-      y2 = fmaf(t_s[(32 + xi + 2) * AS + 32 + kx], xk, y2);
-      y3 = fmaf(t_s[(32 + xi + 3) * AS + 32 + kx], xk, y3);
-    }
-    t_s[(32 + xi + 0) * AS + xj] = -y0;
-    t_s[(32 + xi + 1) * AS + xj] = -y1;
-    t_s[(32 + xi + 2) * AS + xj] = -y2;
-    t_s[(32 + xi + 3) * AS + xj] = -y3;
-  }
-  __syncthreads();
-
-  // ---- Tw = T diag(beta exp(gc)), Tu = T diag(beta) in bf16 (T12 is zero)
-#pragma unroll
-  for (int e = tid; e < C * C; e += 256) {
-    const int i = e >> 6, j = e & 63;
-    const float t = (i < 32 && j >= 32) ? 0.0f : t_s[i * AS + j];
-    tw_s[i * CP + j] = (bf16)(t * be_s[j]);
-    tu_s[i * CP + j] = (bf16)(t * beta_s[j]);
-  }
-  __syncthreads();
-
-  // ---- Tu rows to the workspace; -w^T = -(k^T Tw^T): wave -> 32-row block of
-  // d; the accumulator holds 4 consecutive d of one token row l (8 bytes)
-#pragma unroll
-  for (int e = tid; e < C * C / 8; e += 256) {
-    const int row = e >> 3, c8 = (e & 7) * 8;
-    *reinterpret_cast<u32x4*>(tu_ws + row * C + c8) =
-        *reinterpret_cast<const u32x4*>(tu_s + row * CP + c8);
-  }
-  {
-    const int db = wave;
-#pragma unroll
-    for (int lb = 0; lb < 2; ++lb) {
-      f32x16 aw = {};
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ++ks) {
-        const bf16x8 ak = ld8(kT_s + (db * 32 + col) * CP + ks * 16 + half * 8);
-        const bf16x8 btw = ld8(tw_s + (lb * 32 + col) * CP + ks * 16 + half * 8);
-        aw = mfma(ak, btw, aw);
-      }
-      const int l = lb * 32 + col;
+      const int cs = cb * 32 + col;
+      const float gcs = gc_s[cs];
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        bf16 pw[4];
+        float a4[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pw[e] = (bf16)(-aw[g4 * 4 + e]);
-        const int d = db * 32 + g4 * 8 + half * 4;
-        *reinterpret_cast<uint2*>(w_ws + l * DK + d) = *reinterpret_cast<uint2*>(pw);
+        for (int e = 0; e < 4; ++e) {
+          const int r = g4 * 4 + e;
+          const int cl = rb * 32 + g4 * 8 + half * 4 + e;
+          const float gd = cl >= cs ? exp2f_fast((gc_s[cl] - gcs) * kLog2e) : 0.0f;
+          a4[e] = cl > cs ? beta_s[cl] * gd * kk[r] : 0.0f;
+          aqk_s[cl * CP + cs] = (bf16)(scale * gd * qk[r]);
+        }
+        const int cl0 = rb * 32 + g4 * 8 + half * 4;
+        *reinterpret_cast<float4*>(at_s + cs * AS + cl0) = make_float4(a4[0], a4[1], a4[2], a4[3]);
+      }
+    } else {
+      const int cs = 32 + col;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) aqk_s[((r >> 2) * 8 + half * 4 + (r & 3)) * CP + cs] = (bf16)0.0f;
+    }
+    if (blk + gridDim.x < nblk) load(blk + gridDim.x, cur);  // operands consumed: next chunk
+    __syncthreads();
+
+    // ---- Aqk rows to the workspace (16-byte stores); T = (I + A)^-1, blocked
+    // by 16: the four diagonal blocks Tbb by substitution (wave w: block w,
+    // lane j: column j; p[i] accumulates sum_m A[i][m] T[m][j]), then on fp32
+    // MFMA T10 = -T11 (A10 T00), T32 = -T33 (A32 T22) and, with 32-row
+    // blocks, T21 = -T22 (A21 T11).
+#pragma unroll
+    for (int e = tid; e < C * C / 8; e += 256) {
+      const int row = e >> 3, c8 = (e & 7) * 8;
+      *reinterpret_cast<u32x4*>(aqk_ws + row * C + c8) =
+          *reinterpret_cast<const u32x4*>(aqk_s + row * CP + c8);
+    }
+    {
+      const int base = 16 * wave, jl = lane & 15;
+      float p[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) p[i] = 0.0f;
+      // av[m & 1][gq] = A[base + 4gq .. 4gq + 3][base + m]; step m + 1's
+      // groups are read while step m's FMAs run
+      const float4* a4p = reinterpret_cast<const float4*>(at_s + base * AS + base);
+      float4 av[2][4];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) av[0][gq] = a4p[gq];
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        if (m + 1 < 16) {
+#pragma unroll
+          for (int gq = (m + 2) >> 2; gq < 4; ++gq) av[(m + 1) & 1][gq] = a4p[(m + 1) * (AS / 4) + gq];
+        }
+        const float t = (m == jl ? 1.0f : 0.0f) - p[m];
+        if (lane < 16) t_s[(base + m) * AS + base + jl] = t;
+#pragma unroll
+        for (int gq = (m + 1) >> 2; gq < 4; ++gq) {
+          const float4 a4 = av[m & 1][gq];
+          const int i4 = 4 * gq;
+          if (i4 + 0 > m) p[i4 + 0] = fmaf(a4.x, t, p[i4 + 0]);
+          if (i4 + 1 > m) p[i4 + 1] = fmaf(a4.y, t, p[i4 + 1]);
+          if (i4 + 2 > m) p[i4 + 2] = fmaf(a4.z, t, p[i4 + 2]);
+          if (i4 + 3 > m) p[i4 + 3] = fmaf(a4.w, t, p[i4 + 3]);
+        }
       }
     }
+    __syncthreads();
+    // v_mfma_f32_16x16x4f32 lanes: A[mi][mk], B[mk][mi], D[4 mk + r][mi]
+    const int mi = lane & 15, mk = lane >> 4;
+    if (wave < 2) {  // Y = A10 T00 (wave 0) / A32 T22 (wave 1) -> x_s rows 16 wave ..
+      const int d0 = 32 * wave;
+      f32x4 y = {};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int kx = 4 * kk + mk;
+        y = __builtin_amdgcn_mfma_f32_16x16x4f32(at_s[(d0 + kx) * AS + d0 + 16 + mi],
+                                                t_s[(d0 + kx) * AS + d0 + mi], y, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x_s[(16 * wave + 4 * mk + r) * XS + mi] = y[r];
+    }
+    __syncthreads();
+    if (wave < 2) {  // T10 = -T11 Y (wave 0), T32 = -T33 Y (wave 1)
+      const int d0 = 32 * wave;
+      f32x4 z = {};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int kx = 4 * kk + mk;
+        z = __builtin_amdgcn_mfma_f32_16x16x4f32(t_s[(d0 + 16 + mi) * AS + d0 + 16 + kx],
+                                                x_s[(16 * wave + kx) * XS + mi], z, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) t_s[(d0 + 16 + 4 * mk + r) * AS + d0 + mi] = -z[r];
+    } else {  // the upper blocks T01, T23 are zero
+      const int d0 = 32 * (wave - 2);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) t_s[(d0 + 4 * mk + r) * AS + d0 + 16 + mi] = 0.0f;
+    }
+    __syncthreads();
+    const int qi = wave >> 1, qj = wave & 1;  // 16x16 quadrant of a 32x32 block
+    {  // X = A21 T11 -> x_s
+      f32x4 x = {};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int kx = 4 * kk + mk;
+        x = __builtin_amdgcn_mfma_f32_16x16x4f32(at_s[kx * AS + 32 + 16 * qi + mi],
+                                                t_s[kx * AS + 16 * qj + mi], x, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x_s[(16 * qi + 4 * mk + r) * XS + 16 * qj + mi] = x[r];
+    }
+    __syncthreads();
+    {  // T21 = -T22 X
+      f32x4 y = {};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int kx = 4 * kk + mk;
+        y = __builtin_amdgcn_mfma_f32_16x16x4f32(t_s[(32 + 16 * qi + mi) * AS + 32 + kx],
+                                                x_s[kx * XS + 16 * qj + mi], y, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) t_s[(32 + 16 * qi + 4 * mk + r) * AS + 16 * qj + mi] = -y[r];
+    }
+    __syncthreads();
+
+    // ---- Tw = T diag(beta exp(gc)), Tu = T diag(beta) in bf16 (T12 is zero)
+    // (4 consecutive columns per thread: float4 in, 8-byte bf16 stores out)
+#pragma unroll
+    for (int e = tid; e < C * C / 4; e += 256) {
+      const int i = e >> 4, j = (e & 15) * 4;
+      const float4 t = (i < 32 && j >= 32) ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                                           : *reinterpret_cast<const float4*>(t_s + i * AS + j);
+      const float4 be = *reinterpret_cast<const float4*>(be_s + j);
+      const float4 bt = *reinterpret_cast<const float4*>(beta_s + j);
+      bf16 pw[4] = {(bf16)(t.x * be.x), (bf16)(t.y * be.y), (bf16)(t.z * be.z), (bf16)(t.w * be.w)};
+      bf16 pu[4] = {(bf16)(t.x * bt.x), (bf16)(t.y * bt.y), (bf16)(t.z * bt.z), (bf16)(t.w * bt.w)};
+      *reinterpret_cast<uint2*>(tw_s + i * CP + j) = *reinterpret_cast<uint2*>(pw);
+      *reinterpret_cast<uint2*>(tu_s + i * CP + j) = *reinterpret_cast<uint2*>(pu);
+    }
+    __syncthreads();
+
+    // ---- Tu rows to the workspace; -w^T = -(k^T Tw^T): wave -> 32-row block of
+    // d; the accumulator holds 4 consecutive d of one token row l (8 bytes)
+#pragma unroll
+    for (int e = tid; e < C * C / 8; e += 256) {
+      const int row = e >> 3, c8 = (e & 7) * 8;
+      *reinterpret_cast<u32x4*>(tu_ws + row * C + c8) =
+          *reinterpret_cast<const u32x4*>(tu_s + row * CP + c8);
+    }
+    {
+      const int db = wave;
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb) {
+        f32x16 aw = {};
+#pragma unroll
+        for (int ks = 0; ks < C / 16; ++ks) {
+          const bf16x8 ak = ld8(kT_s + (db * 32 + col) * CP + ks * 16 + half * 8);
+          const bf16x8 btw = ld8(tw_s + (lb * 32 + col) * CP + ks * 16 + half * 8);
+          aw = mfma(ak, btw, aw);
+        }
+        const int l = lb * 32 + col;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          bf16 pw[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pw[e] = (bf16)(-aw[g4 * 4 + e]);
+          const int d = db * 32 + g4 * 8 + half * 4;
+          *reinterpret_cast<uint2*>(w_ws + l * DK + d) = *reinterpret_cast<uint2*>(pw);
+        }
+      }
+    }
+    __syncthreads();  // LDS is rewritten by the next chunk
   }
 }
 
@@ -541,7 +613,7 @@ extern "C" int tileops_gdn_prefill_fwd(const void* q, const void* k, const void*
   const bf16* qb = static_cast<const bf16*>(q);
   const bf16* kb = static_cast<const bf16*>(k);
   if (nblk > 0)
-    gdn::gdn_prep_kernel<<<dim3((unsigned)nblk), dim3(256), 0, s>>>(
+    gdn::gdn_prep_kernel<<<dim3((unsigned)std::min<int64_t>(nblk, 2 * device_cu_count())), dim3(256), 0, s>>>(
         qb, kb, g, beta, static_cast<uint8_t*>(ws), (int)B, (int)T, (int)H, nc, scale);
   gdn::gdn_recur_kernel<<<dim3((unsigned)(B * H * (gdn::DV / gdn::VS))), dim3(256), 0, s>>>(
       qb, kb, static_cast<const bf16*>(v), h0, static_cast<const uint8_t*>(ws),
