@@ -376,16 +376,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // kernel 2: the sequential recurrence over chunks and the output
 // ---------------------------------------------------------------------------
 // Per-chunk operands of one thread, loaded one chunk ahead so that their
-// global-memory latency overlaps the current chunk's work.  Every wavefront
-// runs the same load sequence (only the base pointers differ), which keeps
-// the compiler's wait counts exact.
+// global-memory latency overlaps the current chunk's work.  -w, q, Tu and
+// Aqk are read as whole rows (16 or 8 consecutive lanes per row, every
+// 128-byte line fully used) and staged into LDS, where the MFMA operands are
+// read from; every wavefront runs the same load sequence, which keeps the
+// compiler's wait counts exact.
 struct ChunkOps {
-  bf16x8 a[DK / 16];  // waves 0, 1: rows of -w; waves 2, 3: rows of q
-  bf16x8 m[C / 16];   // waves 0, 1: rows of Tu; waves 2, 3: rows of Aqk
-  u32x4 kr[4];        // k rows 4vg..4vg+3, dims 8vc..8vc+7 (for the decayed k^T)
-  u32x4 vr;           // v row tid / 4, this slice's columns 8 (tid % 4) .. +7
-  float kdec[4];      // gc of those k rows
-  float gc;           // gc of token tid % C
+  u32x4 w[4];    // -w rows 16j + tid / 16, dims 8 (tid % 16) .. +7
+  u32x4 qr[4];   // q rows, same layout
+  u32x4 tu[2];   // Tu rows 32j + tid / 8, columns 8 (tid % 8) .. +7
+  u32x4 aq[2];   // Aqk rows, same layout
+  u32x4 kr[4];   // k rows 4vg..4vg+3, dims 8vc..8vc+7 (for the decayed k^T)
+  u32x4 vr;      // v row tid / 4, this slice's columns 8 (tid % 4) .. +7
+  float kdec[4];  // gc of those k rows
+  float gc;       // gc of token tid % C
   float gc_last;
 };
 
@@ -400,7 +404,14 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
   __shared__ __attribute__((aligned(16))) bf16 kd_s[2][DK * CP];   // (decayed k)^T
   __shared__ __attribute__((aligned(16))) bf16 vt_s[2][VS * CP];   // v^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 ot_s[2][32 * OP];   // output tiles (waves 2, 3)
-  __shared__ float gcb_s[2][C];
+  // -w, q and Tu of the next chunk are written after barrier B, when every
+  // wavefront has finished reading the current ones: one copy each.  Aqk is
+  // still read after barrier B, so it has two slots.
+  __shared__ __attribute__((aligned(16))) bf16 w_s[C * KP];
+  __shared__ __attribute__((aligned(16))) bf16 q_s[C * KP];
+  __shared__ __attribute__((aligned(16))) bf16 tu_s[C * CP];
+  __shared__ __attribute__((aligned(16))) bf16 aqk_s[2][C * CP];
+  __shared__ float qsc_s[2][C];  // scale * exp(gc) per token: the output row factor
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -418,24 +429,33 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
   const int arow = rblk * 32 + col;  // A-operand row of this lane
   const int vg = tid & 15, vc = tid >> 4;
   const int vrow = tid >> 2, vcol = (tid & 3) * 8;
+  const int r16 = tid >> 4, c16 = (tid & 15) * 8;  // 16 lanes per 128-wide row
+  const int r8 = tid >> 3, c8 = (tid & 7) * 8;     // 8 lanes per 64-wide row
 
   auto load = [&](int c, ChunkOps& op) {
     const int t0 = c * C;
     const int last = min(C, T - t0) - 1;  // rows past T read the last row (see below)
     const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
     const float* gc_ws = reinterpret_cast<const float*>(wsc + kGcOff);
+    const bf16* w_g = reinterpret_cast<const bf16*>(wsc + kWOff);
+    const bf16* tu_g = reinterpret_cast<const bf16*>(wsc + kTuOff);
+    const bf16* aqk_g = reinterpret_cast<const bf16*>(wsc + kAqkOff);
+    const bf16* q_g = q + ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK;
     // Rows past T are clamped onto the chunk's last row rather than zeroed:
     // their q only reaches output rows that are not stored, and their k / v
     // only meet rows and columns of W, Tu that are exactly zero (beta = 0).
-    const bf16* abase =
-        wave < 2 ? reinterpret_cast<const bf16*>(wsc + kWOff) + arow * DK
-                 : q + ((int64_t)b * T + t0 + min(arow, last)) * tok_stride + (int64_t)h * DK;
-    const bf16* mbase = reinterpret_cast<const bf16*>(wsc + (wave < 2 ? kTuOff : kAqkOff)) +
-                        arow * C;
 #pragma unroll
-    for (int ks = 0; ks < DK / 16; ++ks) op.a[ks] = ld8(abase + ks * 16 + half * 8);
+    for (int j = 0; j < 4; ++j) {
+      const int row = 16 * j + r16;
+      op.w[j] = *reinterpret_cast<const u32x4*>(w_g + row * DK + c16);
+      op.qr[j] = *reinterpret_cast<const u32x4*>(q_g + min(row, last) * tok_stride + c16);
+    }
 #pragma unroll
-    for (int ks = 0; ks < C / 16; ++ks) op.m[ks] = ld8(mbase + ks * 16 + half * 8);
+    for (int j = 0; j < 2; ++j) {
+      const int row = 32 * j + r8;
+      op.tu[j] = *reinterpret_cast<const u32x4*>(tu_g + row * C + c8);
+      op.aq[j] = *reinterpret_cast<const u32x4*>(aqk_g + row * C + c8);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = min(4 * vg + i, last);
@@ -448,7 +468,8 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
     op.gc = gc_ws[tid & (C - 1)];
     op.gc_last = gc_ws[C - 1];
   };
-  // (decayed k)^T, v^T and gc of a loaded chunk into LDS slot `buf`
+  // (decayed k)^T, v^T, Aqk and gc of a loaded chunk into LDS slot `buf`; -w,
+  // q and Tu into their single copies
   auto stage = [&](const ChunkOps& op, int buf) {
     u32x4 kr[4];
 #pragma unroll
@@ -461,10 +482,20 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
       kr[i] = *reinterpret_cast<u32x4*>(sc);
     }
     store_transposed4x8(kd_s[buf], CP, vc * 8, 4 * vg, kr);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<u32x4*>(w_s + (16 * j + r16) * KP + c16) = op.w[j];
+      *reinterpret_cast<u32x4*>(q_s + (16 * j + r16) * KP + c16) = op.qr[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      *reinterpret_cast<u32x4*>(tu_s + (32 * j + r8) * CP + c8) = op.tu[j];
+      *reinterpret_cast<u32x4*>(aqk_s[buf] + (32 * j + r8) * CP + c8) = op.aq[j];
+    }
     const bf16* ve = reinterpret_cast<const bf16*>(&op.vr);
 #pragma unroll
     for (int j = 0; j < 8; ++j) vt_s[buf][(vcol + j) * CP + vrow] = ve[j];
-    if (tid < C) gcb_s[buf][tid] = op.gc;
+    if (tid < C) qsc_s[buf][tid] = scale * exp2f_fast(op.gc * kLog2e);
   };
 
   // state rows of this wave: d = 32 * wave + (r / 4) * 8 + half * 4 + r % 4
@@ -485,7 +516,7 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
     }
   };
 
-  // one chunk: `cur` holds its operands (staged: kd_s, vt_s, gcb_s [c & 1]);
+  // one chunk: `cur` holds its operands (staged: kd_s, vt_s, qsc_s [c & 1]);
   // `nxt` receives chunk c + 1's
   auto step = [&](int c, const ChunkOps& cur, ChunkOps& nxt) {
     const int buf = c & 1;
@@ -498,11 +529,13 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
     if (wave < 2) {
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks)
-        acc = mfma(cur.m[ks], ld8(vt_s[buf] + col * CP + ks * 16 + half * 8), acc);
+        acc = mfma(ld8(tu_s + arow * CP + ks * 16 + half * 8),
+                   ld8(vt_s[buf] + col * CP + ks * 16 + half * 8), acc);
     }
+    const bf16* alds = (wave < 2 ? w_s : q_s) + arow * KP;
 #pragma unroll
     for (int ks = 0; ks < DK / 16; ++ks)
-      acc = mfma(cur.a[ks], ld8(st_s + col * SP + ks * 16 + half * 8), acc);
+      acc = mfma(ld8(alds + ks * 16 + half * 8), ld8(st_s + col * SP + ks * 16 + half * 8), acc);
     if (wave < 2) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
@@ -516,7 +549,7 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int cl = rblk * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        acc[r] *= scale * exp2f_fast(gcb_s[buf][cl] * kLog2e);
+        acc[r] *= qsc_s[buf][cl];
       }
     }
     __syncthreads();  // W^T visible
@@ -525,7 +558,8 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
     if (wave >= 2) {  // o = scale exp(gc) (q S) + Aqk W, into this wave's LDS tile
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks)
-        acc = mfma(cur.m[ks], ld8(wt_s + col * CP + ks * 16 + half * 8), acc);
+        acc = mfma(ld8(aqk_s[buf] + arow * CP + ks * 16 + half * 8),
+                   ld8(wt_s + col * CP + ks * 16 + half * 8), acc);
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         ot[((r >> 2) * 8 + half * 4 + (r & 3)) * OP + col] = (bf16)acc[r];
