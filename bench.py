@@ -24,6 +24,7 @@ Only one GPU is used; ``--gpus`` above 1 exits with an explanation.
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import os
 import re
@@ -291,9 +292,8 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
-            "bench.py measures one GPU: every operator here is single-device and the "
-            "multi-GPU layout (rows / heads sharded with no exchange) is described in "
-            "DESIGN.md; run with --gpus 1.",
+            "bench.py measures one GPU: every operator here is single-device (across GPUs "
+            "its rows / heads would be sharded with no exchange); run with --gpus 1.",
             file=sys.stderr,
         )
         return 2
@@ -311,10 +311,13 @@ def main() -> int:
                           "launches": args.steps}))
         return 0
 
-    head = bench_headline(args.steps, args.warmup)
-    _log(f"headline GeluAndMulFwdOp: {head['gbs']:.1f} GB/s, {head['kernel_ms'] * 1e3:.1f} us")
-    suite = {} if args.no_suite else bench_suite(args.steps, args.warmup)
-    cpu = None if args.no_cpu_baseline else cpu_baseline_gelu(head["M"], head["N"])
+    # stdout carries the one JSON line only: everything the operators print
+    # while they are built and run goes to stderr
+    with contextlib.redirect_stdout(sys.stderr):
+        head = bench_headline(args.steps, args.warmup)
+        _log(f"headline GeluAndMulFwdOp: {head['gbs']:.1f} GB/s, {head['kernel_ms'] * 1e3:.1f} us")
+        suite = {} if args.no_suite else bench_suite(args.steps, args.warmup)
+        cpu = None if args.no_cpu_baseline else cpu_baseline_gelu(head["M"], head["N"])
 
     line = {
         "metric": METRIC,

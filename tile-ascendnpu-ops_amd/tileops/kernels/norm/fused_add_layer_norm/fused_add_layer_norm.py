@@ -61,7 +61,7 @@ class FusedAddLayerNormKernel(Kernel):
     @property
     def default_config(self) -> dict:
         # one wavefront per row, row held in registers, w/b staged in LDS
-        return {"rows_per_wave": 1, "persistent_blocks_per_cu": 2}
+        return {"rows_per_wave": 1, "rows_per_workgroup": 4}
 
     def forward(
         self,
