@@ -20,14 +20,14 @@
 // beta loaded while the current one is processed): K K^T and Q K^T on bf16
 // MFMA, the 64x64 unit-lower-triangular inverse in fp32 (16x16 diagonal
 // blocks by substitution, one wavefront each, the off-diagonal blocks by
-// products on fp32 MFMA), then w on bf16 MFMA.  -w, Tu, Aqk and gc go to a
-// workspace.
-// Kernel 2 (one workgroup per (b, h, 32-wide slice of V), 4 wavefronts):
-// the state slice lives in MFMA accumulators (wavefront i owns key rows
-// 32i..32i+31), its bf16 copy and W are exchanged through LDS.  Every
-// wavefront loads the next chunk's operands with the same instruction
-// sequence while the current chunk runs; waves 0, 1 form W (rows 0-31,
-// 32-63), waves 2, 3 the output rows.  Two workgroup barriers per chunk.
+// products on fp32 MFMA), then w on bf16 MFMA.  -w, Tu, Aqk, the decayed
+// keys (k e^{gc_C - gc})^T and the per-token factors go to a workspace.
+// Kernel 2 (one workgroup per (b, h, 32-wide slice of V), 8 wavefronts):
+// four compute wavefronts keep the state slice in MFMA accumulators
+// (wavefront i owns key rows 32i..32i+31) and exchange its bf16 copy and W
+// through LDS; waves 0, 1 form W (rows 0-31, 32-63), waves 2, 3 the output
+// rows.  Four loader wavefronts bring the next chunk's operands into LDS
+// with direct-to-LDS loads meanwhile.  Two workgroup barriers per chunk.
 #include "common.h"
 
 namespace tileops {
@@ -45,11 +45,13 @@ constexpr int CP = C + 8;   // LDS row stride of a transposed [*][C] tile (eleme
 constexpr float kLog2e = 1.4426950408889634f;
 
 // workspace per chunk
-constexpr size_t kWOff = 0;                                   // -w  [C][DK] bf16
-constexpr size_t kTuOff = kWOff + (size_t)C * DK * 2;         // Tu  [C][C]  bf16
-constexpr size_t kAqkOff = kTuOff + (size_t)C * C * 2;        // Aqk [C][C]  bf16
-constexpr size_t kGcOff = kAqkOff + (size_t)C * C * 2;        // gc  [C]     f32
-constexpr size_t kChunkBytes = kGcOff + (size_t)C * 4;
+constexpr size_t kWOff = 0;                                   // -w   [C][DK] bf16
+constexpr size_t kTuOff = kWOff + (size_t)C * DK * 2;         // Tu   [C][C]  bf16
+constexpr size_t kAqkOff = kTuOff + (size_t)C * C * 2;        // Aqk  [C][C]  bf16
+constexpr size_t kKdOff = kAqkOff + (size_t)C * C * 2;        // kd^T [DK][C] bf16
+constexpr size_t kFacOff = kKdOff + (size_t)DK * C * 2;       // factors, f32 [kFacN]
+constexpr int kFacN = 80;  // scale e^{gc_l} (l < C), e^{gc_C} at index C, zero pad
+constexpr size_t kChunkBytes = kFacOff + (size_t)kFacN * 4;
 
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -109,7 +111,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(16))) float x_s[32 * XS];
   __shared__ __attribute__((aligned(16))) bf16 kT_s[DK * CP];
   __shared__ __attribute__((aligned(16))) bf16 aqk_s[C * CP];
-  __shared__ __attribute__((aligned(16))) float gc_s[C], beta_s[C], be_s[C];
+  __shared__ __attribute__((aligned(16))) float gc_s[C], beta_s[C], be_s[C], dec_s[C];
   static_assert(C * KP * 2 <= C * AS * 4, "k tile must fit the T region");
   static_assert(2 * C * CP * 2 <= C * AS * 4, "Tw and Tu must fit the A region");
   bf16* k_s = reinterpret_cast<bf16*>(r0);
@@ -156,7 +158,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     bf16* w_ws = reinterpret_cast<bf16*>(wsc + kWOff);
     bf16* tu_ws = reinterpret_cast<bf16*>(wsc + kTuOff);
     bf16* aqk_ws = reinterpret_cast<bf16*>(wsc + kAqkOff);
-    float* gc_ws = reinterpret_cast<float*>(wsc + kGcOff);
+    bf16* kd_ws = reinterpret_cast<bf16*>(wsc + kKdOff);
+    float* fac_ws = reinterpret_cast<float*>(wsc + kFacOff);
     u32x4 (&kr)[4] = cur.kr;
 
     // ---- stage k (natural + transposed); rows past T are 0
@@ -180,7 +183,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       gc_s[lane] = x;
       beta_s[lane] = bt;
       be_s[lane] = bt * exp2f_fast(x * kLog2e);
-      gc_ws[lane] = x;
+      // factors the recurrence applies: scale e^{gc} per output row, the
+      // chunk decay e^{gc_C}, and e^{gc_C - gc} for the decayed keys
+      const float gl = __shfl(x, C - 1, 64);
+      dec_s[lane] = exp2f_fast((gl - x) * kLog2e);
+      fac_ws[lane] = scale * exp2f_fast(x * kLog2e);
+      if (lane < kFacN - C) fac_ws[C + lane] = lane == 0 ? exp2f_fast(gl * kLog2e) : 0.0f;
     }
     __syncthreads();
 
@@ -368,6 +376,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
+    // ---- (decayed k)^T = (e^{gc_C - gc} o k)^T to the workspace, [DK][C]
+    // rows of 16-byte chunks (k rows past T are zero already)
+#pragma unroll
+    for (int j = 0; j < DK * C / 8 / 256; ++j) {
+      const int idx = tid + 256 * j;
+      const int d = idx >> 3, c8 = (idx & 7) * 8;
+      const bf16x8 kv = ld8(kT_s + d * CP + c8);
+      const float4 f0 = *reinterpret_cast<const float4*>(dec_s + c8);
+      const float4 f1 = *reinterpret_cast<const float4*>(dec_s + c8 + 4);
+      bf16x8 o8;
+      o8[0] = (bf16)((float)kv[0] * f0.x); o8[1] = (bf16)((float)kv[1] * f0.y);
+      o8[2] = (bf16)((float)kv[2] * f0.z); o8[3] = (bf16)((float)kv[3] * f0.w);
+      o8[4] = (bf16)((float)kv[4] * f1.x); o8[5] = (bf16)((float)kv[5] * f1.y);
+      o8[6] = (bf16)((float)kv[6] * f1.z); o8[7] = (bf16)((float)kv[7] * f1.w);
+      *reinterpret_cast<bf16x8*>(kd_ws + d * C + c8) = o8;
+    }
     __syncthreads();  // LDS is rewritten by the next chunk
   }
 }
@@ -375,47 +399,81 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // ---------------------------------------------------------------------------
 // kernel 2: the sequential recurrence over chunks and the output
 // ---------------------------------------------------------------------------
-// Per-chunk operands of one thread, loaded one chunk ahead so that their
-// global-memory latency overlaps the current chunk's work.  -w, q, Tu and
-// Aqk are read as whole rows (16 or 8 consecutive lanes per row, every
-// 128-byte line fully used) and staged into LDS, where the MFMA operands are
-// read from; every wavefront runs the same load sequence, which keeps the
-// compiler's wait counts exact.
-struct ChunkOps {
-  u32x4 w[4];    // -w rows 16j + tid / 16, dims 8 (tid % 16) .. +7
-  u32x4 qr[4];   // q rows, same layout
-  u32x4 tu[2];   // Tu rows 32j + tid / 8, columns 8 (tid % 8) .. +7
-  u32x4 aq[2];   // Aqk rows, same layout
-  u32x4 kr[4];   // k rows 4vg..4vg+3, dims 8vc..8vc+7 (for the decayed k^T)
-  u32x4 vr;      // v row tid / 4, this slice's columns 8 (tid % 4) .. +7
-  float kdec[4];  // gc of those k rows
-  float gc;       // gc of token tid % C
-  float gc_last;
+// LDS images of one chunk's operands.  They are filled straight from memory
+// by direct-to-LDS loads (global_load_lds_dwordx4: the 16 bytes of lane l
+// land at base + 16 l, every lane choosing its own source address), one
+// chunk ahead, into two slots.  Rows are stored unpadded with their 16-byte
+// chunks XOR-swizzled by row, so that an MFMA operand read (16 consecutive
+// rows, one chunk each) touches 16 distinct bank groups.
+struct ChunkSlot {
+  bf16 w[C * DK];    // -w rows l: chunk p of row l holds chunk p ^ (l & 15)
+  bf16 q[C * DK];    // q rows, same swizzle
+  bf16 tu[C * C];    // Tu rows: chunk p holds chunk p ^ ((l >> 1) & 7)
+  bf16 aqk[C * C];   // Aqk rows, same
+  bf16 kd[DK * C];   // (decayed k)^T rows d, same
+  float fac[kFacN];  // scale e^{gc_l} (l < C), e^{gc_C} at [C]
 };
 
-__global__ __launch_bounds__(256) void gdn_recur_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const float* __restrict__ h0, const uint8_t* __restrict__ ws, bf16* __restrict__ o,
-    float* __restrict__ hT, int B, int T, int H, int NC, float scale) {
+// element offset of 16-byte chunk `kc` of row `r` in a swizzled image with
+// 128-element (16-chunk) or 64-element (8-chunk) rows
+__device__ __forceinline__ int swz16(int r, int kc) { return r * DK + ((kc ^ (r & 15)) << 3); }
+__device__ __forceinline__ int swz8(int r, int kc) { return r * C + ((kc ^ ((r >> 1) & 7)) << 3); }
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// Workgroup barrier that waits only for this wavefront's LDS accesses
+// (lgkmcnt(0); vmcnt and expcnt left at their maxima), so that direct-to-LDS
+// loads issued before it stay in flight across it.  __syncthreads() would
+// also wait for them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Fill the swizzled image `dst` (NCH 16-byte chunks, CPR per row) from the
+// rows `src + min(r, rmax) * stride` (elements).  Each of the 4 wavefronts
+// issues every 4th 1 KB window (64 chunks).
+template <int CPR, int NCH>
+__device__ __forceinline__ void gather_rows(bf16* dst, const bf16* src, int64_t stride, int rmax,
+                                            int wave, int lane) {
+  static_assert(NCH % 256 == 0, "whole windows for every wavefront");
+#pragma unroll
+  for (int i = 0; i < NCH / 256; ++i) {
+    const int win = 4 * i + wave;
+    const int ch = win * 64 + lane;
+    const int r = ch / CPR, p = ch % CPR;
+    const int key = CPR == 16 ? (r & 15) : ((r >> 1) & 7);
+    const bf16* g = src + (int64_t)min(r, rmax) * stride + ((p ^ key) << 3);
+    __builtin_amdgcn_global_load_lds(g, (lds_void_ptr)(dst + win * 512), 16, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(512) void gdn_recur_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ v, const float* __restrict__ h0,
+    const uint8_t* __restrict__ ws, bf16* __restrict__ o, float* __restrict__ hT, int B, int T,
+    int H, int NC) {
   constexpr int SP = DK + 8;  // row stride of S^T [v][d]
   constexpr int OP = VS + 8;  // row stride of an output tile [token][v]
+  // two separate objects, so that the compiler can tell a slot being read
+  // from the one the direct-to-LDS loads are filling
+  __shared__ __attribute__((aligned(16))) ChunkSlot slot0;
+  __shared__ __attribute__((aligned(16))) ChunkSlot slot1;
   __shared__ __attribute__((aligned(16))) bf16 st_s[VS * SP];      // bf16 S^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 wt_s[VS * CP];      // bf16 W^T (slice)
-  __shared__ __attribute__((aligned(16))) bf16 kd_s[2][DK * CP];   // (decayed k)^T
   __shared__ __attribute__((aligned(16))) bf16 vt_s[2][VS * CP];   // v^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 ot_s[2][32 * OP];   // output tiles (waves 2, 3)
-  // -w, q and Tu of the next chunk are written after barrier B, when every
-  // wavefront has finished reading the current ones: one copy each.  Aqk is
-  // still read after barrier B, so it has two slots.
-  __shared__ __attribute__((aligned(16))) bf16 w_s[C * KP];
-  __shared__ __attribute__((aligned(16))) bf16 q_s[C * KP];
-  __shared__ __attribute__((aligned(16))) bf16 tu_s[C * CP];
-  __shared__ __attribute__((aligned(16))) bf16 aqk_s[2][C * CP];
-  __shared__ float qsc_s[2][C];  // scale * exp(gc) per token: the output row factor
 
+  // waves 0-3 compute; waves 4-7 (one per SIMD beside them) only move the
+  // next chunk's operands, so that the bounded rate of the CU's load path
+  // never holds up a compute wavefront's instruction stream
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool loader = wave >= 4;
+  const int lw = wave & 3;     // index among the loaders / among the compute waves
+  const int ltid = tid & 255;  // thread index inside its group of four wavefronts
   const int col = lane & 31, half = lane >> 5;
-  // the VS-slices of one head run on the same XCD (they share q, k, w, Aqk)
+  // the VS-slices of one head run on the same XCD (they share q, w, Aqk, kd)
   const int total = gridDim.x;
   int id = blockIdx.x;
   if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
@@ -427,83 +485,49 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
   const int64_t tok_stride = (int64_t)H * DK;
   const int rblk = wave & 1;         // chunk rows 32*rblk .. 32*rblk+31 (A operands)
   const int arow = rblk * 32 + col;  // A-operand row of this lane
-  const int vg = tid & 15, vc = tid >> 4;
-  const int vrow = tid >> 2, vcol = (tid & 3) * 8;
-  const int r16 = tid >> 4, c16 = (tid & 15) * 8;  // 16 lanes per 128-wide row
-  const int r8 = tid >> 3, c8 = (tid & 7) * 8;     // 8 lanes per 64-wide row
+  const int vrow = ltid >> 2, vcol = (ltid & 3) * 8;
 
-  auto load = [&](int c, ChunkOps& op) {
+  // chunk c's operands (loader wavefronts): the LDS images of slot `sl`
+  // (direct loads) and this thread's 16 bytes of the v slice (register,
+  // transposed into LDS later)
+  auto load = [&](int c, ChunkSlot& sl, u32x4& vr) {
     const int t0 = c * C;
     const int last = min(C, T - t0) - 1;  // rows past T read the last row (see below)
     const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
-    const float* gc_ws = reinterpret_cast<const float*>(wsc + kGcOff);
-    const bf16* w_g = reinterpret_cast<const bf16*>(wsc + kWOff);
-    const bf16* tu_g = reinterpret_cast<const bf16*>(wsc + kTuOff);
-    const bf16* aqk_g = reinterpret_cast<const bf16*>(wsc + kAqkOff);
-    const bf16* q_g = q + ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK;
     // Rows past T are clamped onto the chunk's last row rather than zeroed:
-    // their q only reaches output rows that are not stored, and their k / v
-    // only meet rows and columns of W, Tu that are exactly zero (beta = 0).
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 16 * j + r16;
-      op.w[j] = *reinterpret_cast<const u32x4*>(w_g + row * DK + c16);
-      op.qr[j] = *reinterpret_cast<const u32x4*>(q_g + min(row, last) * tok_stride + c16);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int row = 32 * j + r8;
-      op.tu[j] = *reinterpret_cast<const u32x4*>(tu_g + row * C + c8);
-      op.aq[j] = *reinterpret_cast<const u32x4*>(aqk_g + row * C + c8);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = min(4 * vg + i, last);
-      op.kr[i] = *reinterpret_cast<const u32x4*>(k + ((int64_t)b * T + t0 + row) * tok_stride +
-                                                 (int64_t)h * DK + vc * 8);
-      op.kdec[i] = gc_ws[4 * vg + i];
-    }
-    op.vr = *reinterpret_cast<const u32x4*>(
+    // their q only reaches output rows that are not stored, and their v only
+    // meets columns of Tu that are exactly zero (beta = 0).
+    vr = *reinterpret_cast<const u32x4*>(
         v + ((int64_t)b * T + t0 + min(vrow, last)) * tok_stride + (int64_t)h * DV + v0 + vcol);
-    op.gc = gc_ws[tid & (C - 1)];
-    op.gc_last = gc_ws[C - 1];
+    gather_rows<16, C * DK / 8>(sl.w, reinterpret_cast<const bf16*>(wsc + kWOff), DK, C - 1, lw,
+                                lane);
+    gather_rows<16, C * DK / 8>(sl.q, q + ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK,
+                                tok_stride, last, lw, lane);
+    gather_rows<8, C * C / 8>(sl.tu, reinterpret_cast<const bf16*>(wsc + kTuOff), C, C - 1, lw,
+                              lane);
+    gather_rows<8, C * C / 8>(sl.aqk, reinterpret_cast<const bf16*>(wsc + kAqkOff), C, C - 1, lw,
+                              lane);
+    gather_rows<8, DK * C / 8>(sl.kd, reinterpret_cast<const bf16*>(wsc + kKdOff), C, DK - 1, lw,
+                               lane);
+    if (lw == 0 && lane < kFacN / 4)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const float*>(wsc + kFacOff) + lane * 4,
+                                       (lds_void_ptr)sl.fac, 16, 0, 0);
   };
-  // (decayed k)^T, v^T, Aqk and gc of a loaded chunk into LDS slot `buf`; -w,
-  // q and Tu into their single copies
-  auto stage = [&](const ChunkOps& op, int buf) {
-    u32x4 kr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float f = exp2f_fast((op.gc_last - op.kdec[i]) * kLog2e);
-      const bf16* e = reinterpret_cast<const bf16*>(&op.kr[i]);
-      bf16 sc[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sc[j] = (bf16)((float)e[j] * f);
-      kr[i] = *reinterpret_cast<u32x4*>(sc);
-    }
-    store_transposed4x8(kd_s[buf], CP, vc * 8, 4 * vg, kr);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      *reinterpret_cast<u32x4*>(w_s + (16 * j + r16) * KP + c16) = op.w[j];
-      *reinterpret_cast<u32x4*>(q_s + (16 * j + r16) * KP + c16) = op.qr[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      *reinterpret_cast<u32x4*>(tu_s + (32 * j + r8) * CP + c8) = op.tu[j];
-      *reinterpret_cast<u32x4*>(aqk_s[buf] + (32 * j + r8) * CP + c8) = op.aq[j];
-    }
-    const bf16* ve = reinterpret_cast<const bf16*>(&op.vr);
+  // v^T of a loaded chunk into LDS slot `buf`
+  auto stage_v = [&](const u32x4& vr, int buf) {
+    const bf16* ve = reinterpret_cast<const bf16*>(&vr);
 #pragma unroll
     for (int j = 0; j < 8; ++j) vt_s[buf][(vcol + j) * CP + vrow] = ve[j];
-    if (tid < C) qsc_s[buf][tid] = scale * exp2f_fast(op.gc * kLog2e);
   };
 
-  // state rows of this wave: d = 32 * wave + (r / 4) * 8 + half * 4 + r % 4
-  f32x16 s_acc;
+  // state rows of a compute wave: d = 32 * wave + (r / 4) * 8 + half * 4 + r % 4
+  f32x16 s_acc = {};
+  if (!loader) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int d = 32 * wave + (r >> 2) * 8 + half * 4 + (r & 3);
-    s_acc[r] = h0 ? h0[(((int64_t)b * H + h) * DK + d) * DV + v0 + col] : 0.0f;
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * wave + (r >> 2) * 8 + half * 4 + (r & 3);
+      s_acc[r] = h0 ? h0[(((int64_t)b * H + h) * DK + d) * DV + v0 + col] : 0.0f;
+    }
   }
   auto publish_state = [&]() {
 #pragma unroll
@@ -516,26 +540,38 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
     }
   };
 
-  // one chunk: `cur` holds its operands (staged: kd_s, vt_s, qsc_s [c & 1]);
-  // `nxt` receives chunk c + 1's
-  auto step = [&](int c, const ChunkOps& cur, ChunkOps& nxt) {
+  // one chunk: `cur` holds its operands (and vt_s[c & 1], st_s); the loader
+  // wavefronts fill `nxt` and vt_s[(c + 1) & 1] meanwhile
+  auto step = [&](int c, const ChunkSlot& cur, ChunkSlot& nxt) {
     const int buf = c & 1;
+    const bool more = c + 1 < NC;
+    if (loader) {
+      u32x4 vr;
+      if (more) load(c + 1, nxt, vr);
+      lds_barrier();  // (barrier B)
+      if (more) stage_v(vr, buf ^ 1);
+      // a wavefront's counters cover only its own loads: each loader waits
+      // for its share of the next chunk's images before the barrier
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();  // (barrier A)
+      return;
+    }
     const int t0 = c * C;
     const int n = min(C, T - t0);
-    if (c + 1 < NC) load(c + 1, nxt);
 
     // waves 0, 1: W = Tu v - w S (rows 32 rblk ..); waves 2, 3: q S
     f32x16 acc = {};
     if (wave < 2) {
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks)
-        acc = mfma(ld8(tu_s + arow * CP + ks * 16 + half * 8),
+        acc = mfma(ld8(cur.tu + swz8(arow, ks * 2 + half)),
                    ld8(vt_s[buf] + col * CP + ks * 16 + half * 8), acc);
     }
-    const bf16* alds = (wave < 2 ? w_s : q_s) + arow * KP;
+    const bf16* abase = wave < 2 ? cur.w : cur.q;
 #pragma unroll
     for (int ks = 0; ks < DK / 16; ++ks)
-      acc = mfma(ld8(alds + ks * 16 + half * 8), ld8(st_s + col * SP + ks * 16 + half * 8), acc);
+      acc = mfma(ld8(abase + swz16(arow, ks * 2 + half)), ld8(st_s + col * SP + ks * 16 + half * 8),
+                 acc);
     if (wave < 2) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
@@ -549,30 +585,29 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int cl = rblk * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        acc[r] *= qsc_s[buf][cl];
+        acc[r] *= cur.fac[cl];
       }
     }
-    __syncthreads();  // W^T visible
+    lds_barrier();  // (barrier B) W^T visible
 
     bf16* ot = ot_s[wave & 1];
     if (wave >= 2) {  // o = scale exp(gc) (q S) + Aqk W, into this wave's LDS tile
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks)
-        acc = mfma(ld8(aqk_s[buf] + arow * CP + ks * 16 + half * 8),
+        acc = mfma(ld8(cur.aqk + swz8(arow, ks * 2 + half)),
                    ld8(wt_s + col * CP + ks * 16 + half * 8), acc);
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         ot[((r >> 2) * 8 + half * 4 + (r & 3)) * OP + col] = (bf16)acc[r];
     }
     // S <- exp(gc_C) S + (decayed k)^T W   (rows 32 * wave .. of the state)
-    const float dec = exp2f_fast(cur.gc_last * kLog2e);
+    const float dec = cur.fac[C];
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_acc[r] *= dec;
 #pragma unroll
     for (int ks = 0; ks < C / 16; ++ks)
-      s_acc = mfma(ld8(kd_s[buf] + (32 * wave + col) * CP + ks * 16 + half * 8),
+      s_acc = mfma(ld8(cur.kd + swz8(32 * wave + col, ks * 2 + half)),
                    ld8(wt_s + col * CP + ks * 16 + half * 8), s_acc);
-    if (c + 1 < NC) stage(nxt, buf ^ 1);
     publish_state();
     // output rows leave last, as 16-byte stores: nothing above waits on them
     if (wave >= 2) {
@@ -586,23 +621,25 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(
               *reinterpret_cast<const u32x4*>(ot + rr * OP + cc);
       }
     }
-    __syncthreads();  // next chunk's S^T, (decayed k)^T, v^T and gc visible
+    __syncthreads();  // (barrier A) next chunk's images, S^T and v^T visible
   };
 
-  ChunkOps ops_a, ops_b;
-  if (NC > 0) {
-    load(0, ops_a);
-    stage(ops_a, 0);
+  if (NC > 0 && loader) {
+    u32x4 vr;
+    load(0, slot0, vr);
+    stage_v(vr, 0);
+    __builtin_amdgcn_s_waitcnt(0);
   }
-  publish_state();
+  if (!loader) publish_state();
   __syncthreads();
   int c = 0;
   for (; c + 1 < NC; c += 2) {
-    step(c, ops_a, ops_b);
-    step(c + 1, ops_b, ops_a);
+    step(c, slot0, slot1);
+    step(c + 1, slot1, slot0);
   }
-  if (c < NC) step(c, ops_a, ops_b);
+  if (c < NC) step(c, slot0, slot1);
 
+  if (loader) return;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int d = 32 * wave + (r >> 2) * 8 + half * 4 + (r & 3);
@@ -649,8 +686,8 @@ extern "C" int tileops_gdn_prefill_fwd(const void* q, const void* k, const void*
   if (nblk > 0)
     gdn::gdn_prep_kernel<<<dim3((unsigned)std::min<int64_t>(nblk, 2 * device_cu_count())), dim3(256), 0, s>>>(
         qb, kb, g, beta, static_cast<uint8_t*>(ws), (int)B, (int)T, (int)H, nc, scale);
-  gdn::gdn_recur_kernel<<<dim3((unsigned)(B * H * (gdn::DV / gdn::VS))), dim3(256), 0, s>>>(
-      qb, kb, static_cast<const bf16*>(v), h0, static_cast<const uint8_t*>(ws),
-      static_cast<bf16*>(o), hT, (int)B, (int)T, (int)H, nc, scale);
+  gdn::gdn_recur_kernel<<<dim3((unsigned)(B * H * (gdn::DV / gdn::VS))), dim3(512), 0, s>>>(
+      qb, static_cast<const bf16*>(v), h0, static_cast<const uint8_t*>(ws),
+      static_cast<bf16*>(o), hT, (int)B, (int)T, (int)H, nc);
   return launch_status();
 }
