@@ -464,6 +464,7 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
   __shared__ __attribute__((aligned(16))) bf16 wt_s[VS * CP];      // bf16 W^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 vt_s[2][VS * CP];   // v^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 ot_s[2][32 * OP];   // output tiles (waves 2, 3)
+  __shared__ __attribute__((aligned(16))) uint32_t touch_s[64];    // landing area of L2 prefetches
 
   // waves 0-3 compute; waves 4-7 (one per SIMD beside them) only move the
   // next chunk's operands, so that the bounded rate of the CU's load path
@@ -513,6 +514,32 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const float*>(wsc + kFacOff) + lane * 4,
                                        (lds_void_ptr)sl.fac, 16, 0, 0);
   };
+  // L2 prefetch of chunk c (loader wavefronts): one 4-byte load per 128-byte
+  // line of its workspace record and q rows (the four V-slices of a head
+  // share them, every fourth line each) and of this slice's v rows, landing
+  // in a scratch LDS word.  Every thread issues exactly one (spare threads
+  // repeat a line), so the wait counts stay exact.
+  auto touch = [&](int c) {
+    constexpr int kWsLines = (int)((kChunkBytes + 127) / 128);
+    constexpr int kShared = kWsLines + 2 * C;  // + q rows, two lines each
+    constexpr int kPerSlice = (kShared + 3) / 4;
+    const int t0 = c * C;
+    const int last = min(C, T - t0) - 1;
+    const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
+    const void* a;
+    const int j = min(ltid, kPerSlice - 1) * 4 + vs;
+    if (ltid < kPerSlice && j < kShared) {
+      a = j < kWsLines ? static_cast<const void*>(wsc + (size_t)j * 128)
+                       : static_cast<const void*>(
+                             q + ((int64_t)b * T + t0 + min((j - kWsLines) >> 1, last)) *
+                                     tok_stride +
+                             (int64_t)h * DK + ((j - kWsLines) & 1) * 64);
+    } else {
+      const int r = min(max(ltid - kPerSlice, 0), C - 1);
+      a = v + ((int64_t)b * T + t0 + min(r, last)) * tok_stride + (int64_t)h * DV + v0;
+    }
+    __builtin_amdgcn_global_load_lds(a, (lds_void_ptr)touch_s, 4, 0, 0);
+  };
   // v^T of a loaded chunk into LDS slot `buf`
   auto stage_v = [&](const u32x4& vr, int buf) {
     const bf16* ve = reinterpret_cast<const bf16*>(&vr);
@@ -546,14 +573,19 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
     const int buf = c & 1;
     const bool more = c + 1 < NC;
     if (loader) {
+      // chunk c + 1 into `nxt` (past the end: the last chunk again, never
+      // read); after v^T is staged, the L2 prefetch of chunk c + 2.  Both are
+      // unconditional so that the wait counts stay exact
       u32x4 vr;
-      if (more) load(c + 1, nxt, vr);
+      load(more ? c + 1 : NC - 1, nxt, vr);
       lds_barrier();  // (barrier B)
       if (more) stage_v(vr, buf ^ 1);
+      touch(min(c + 2, NC - 1));
       // a wavefront's counters cover only its own loads: each loader waits
-      // for its share of the next chunk's images before the barrier
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();  // (barrier A)
+      // for its share of the next chunk's images (everything but the one
+      // prefetch issued last: vmcnt(1)) before the barrier
+      __builtin_amdgcn_s_waitcnt(0x0F71);
+      lds_barrier();  // (barrier A)
       return;
     }
     const int t0 = c * C;
@@ -621,17 +653,18 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
               *reinterpret_cast<const u32x4*>(ot + rr * OP + cc);
       }
     }
-    __syncthreads();  // (barrier A) next chunk's images, S^T and v^T visible
+    lds_barrier();  // (barrier A) next chunk's images, S^T and v^T visible
   };
 
   if (NC > 0 && loader) {
     u32x4 vr;
     load(0, slot0, vr);
     stage_v(vr, 0);
-    __builtin_amdgcn_s_waitcnt(0);
+    touch(min(1, NC - 1));
+    __builtin_amdgcn_s_waitcnt(0x0F71);
   }
   if (!loader) publish_state();
-  __syncthreads();
+  lds_barrier();
   int c = 0;
   for (; c + 1 < NC; c += 2) {
     step(c, slot0, slot1);
@@ -639,7 +672,10 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
   }
   if (c < NC) step(c, slot0, slot1);
 
-  if (loader) return;
+  if (loader) {
+    __builtin_amdgcn_s_waitcnt(0);  // no load may land after the workgroup's LDS is released
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int d = 32 * wave + (r >> 2) * 8 + half * 4 + (r & 3);
