@@ -455,7 +455,6 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
     const uint8_t* __restrict__ ws, bf16* __restrict__ o, float* __restrict__ hT, int B, int T,
     int H, int NC) {
   constexpr int SP = DK + 8;  // row stride of S^T [v][d]
-  constexpr int OP = VS + 8;  // row stride of an output tile [token][v]
   // two separate objects, so that the compiler can tell a slot being read
   // from the one the direct-to-LDS loads are filling
   __shared__ __attribute__((aligned(16))) ChunkSlot slot0;
@@ -463,7 +462,6 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
   __shared__ __attribute__((aligned(16))) bf16 st_s[VS * SP];      // bf16 S^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 wt_s[VS * CP];      // bf16 W^T (slice)
   __shared__ __attribute__((aligned(16))) bf16 vt_s[2][VS * CP];   // v^T (slice)
-  __shared__ __attribute__((aligned(16))) bf16 ot_s[2][32 * OP];   // output tiles (waves 2, 3)
   __shared__ __attribute__((aligned(16))) uint32_t touch_s[64];    // landing area of L2 prefetches
 
   // waves 0-3 compute; waves 4-7 (one per SIMD beside them) only move the
@@ -591,20 +589,20 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
     const int t0 = c * C;
     const int n = min(C, T - t0);
 
-    // waves 0, 1: W = Tu v - w S (rows 32 rblk ..); waves 2, 3: q S
+    // waves 0, 1: W = Tu v - w S (rows 32 rblk ..); waves 2, 3: the output
+    // in the transposed orientation, o^T = S^T q^T (tokens 32 rblk ..), so
+    // that a lane owns one token: its row factor is one scalar and its 16
+    // values are 4 runs of 4 consecutive v, stored straight to memory
     f32x16 acc = {};
     if (wave < 2) {
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks)
         acc = mfma(ld8(cur.tu + swz8(arow, ks * 2 + half)),
                    ld8(vt_s[buf] + col * CP + ks * 16 + half * 8), acc);
-    }
-    const bf16* abase = wave < 2 ? cur.w : cur.q;
 #pragma unroll
-    for (int ks = 0; ks < DK / 16; ++ks)
-      acc = mfma(ld8(abase + swz16(arow, ks * 2 + half)), ld8(st_s + col * SP + ks * 16 + half * 8),
-                 acc);
-    if (wave < 2) {
+      for (int ks = 0; ks < DK / 16; ++ks)
+        acc = mfma(ld8(cur.w + swz16(arow, ks * 2 + half)),
+                   ld8(st_s + col * SP + ks * 16 + half * 8), acc);
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         bf16 p[4];
@@ -615,22 +613,30 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
       }
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int cl = rblk * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        acc[r] *= cur.fac[cl];
-      }
+      for (int ks = 0; ks < DK / 16; ++ks)
+        acc = mfma(ld8(st_s + col * SP + ks * 16 + half * 8),
+                   ld8(cur.q + swz16(arow, ks * 2 + half)), acc);
+      const float f = cur.fac[arow];  // scale e^{gc} of this lane's token
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] *= f;
     }
     lds_barrier();  // (barrier B) W^T visible
 
-    bf16* ot = ot_s[wave & 1];
-    if (wave >= 2) {  // o = scale exp(gc) (q S) + Aqk W, into this wave's LDS tile
+    if (wave >= 2) {  // o^T += W^T Aqk^T, then this lane's token row to memory
 #pragma unroll
       for (int ks = 0; ks < C / 16; ++ks)
-        acc = mfma(ld8(cur.aqk + swz8(arow, ks * 2 + half)),
-                   ld8(wt_s + col * CP + ks * 16 + half * 8), acc);
+        acc = mfma(ld8(wt_s + col * CP + ks * 16 + half * 8),
+                   ld8(cur.aqk + swz8(arow, ks * 2 + half)), acc);
+      if (arow < n) {
+        bf16* orow = o + ((int64_t)b * T + t0 + arow) * tok_stride + (int64_t)h * DV + v0;
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        ot[((r >> 2) * 8 + half * 4 + (r & 3)) * OP + col] = (bf16)acc[r];
+        for (int g4 = 0; g4 < 4; ++g4) {
+          bf16 p[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) p[e] = (bf16)acc[g4 * 4 + e];
+          *reinterpret_cast<uint2*>(orow + g4 * 8 + half * 4) = *reinterpret_cast<uint2*>(p);
+        }
+      }
     }
     // S <- exp(gc_C) S + (decayed k)^T W   (rows 32 * wave .. of the state)
     const float dec = cur.fac[C];
@@ -641,18 +647,6 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
       s_acc = mfma(ld8(cur.kd + swz8(32 * wave + col, ks * 2 + half)),
                    ld8(wt_s + col * CP + ks * 16 + half * 8), s_acc);
     publish_state();
-    // output rows leave last, as 16-byte stores: nothing above waits on them
-    if (wave >= 2) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int rr = i * 16 + (lane >> 2), cc = (lane & 3) * 8;
-        const int cl = rblk * 32 + rr;
-        if (cl < n)
-          *reinterpret_cast<u32x4*>(o + ((int64_t)b * T + t0 + cl) * tok_stride +
-                                    (int64_t)h * DV + v0 + cc) =
-              *reinterpret_cast<const u32x4*>(ot + rr * OP + cc);
-      }
-    }
     lds_barrier();  // (barrier A) next chunk's images, S^T and v^T visible
   };
 
