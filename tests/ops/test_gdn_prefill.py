@@ -42,6 +42,11 @@ def _check(inputs, o, hT, h0, scale, pairs):
         pytest.param(1, 200, 2, True, marks=pytest.mark.full),  # ragged last chunk
         pytest.param(2, 1000, 3, True, marks=pytest.mark.full),
         pytest.param(1, 37, 1, True, marks=pytest.mark.full),   # shorter than a chunk
+        # odd chunk counts (the recurrence runs chunks in pairs plus a tail)
+        # and workgroup counts that are not a multiple of the 8 XCDs
+        pytest.param(1, 130, 2, True, marks=pytest.mark.full),   # 3 chunks, ragged
+        pytest.param(2, 320, 1, False, marks=pytest.mark.full),  # 5 chunks
+        pytest.param(1, 128, 5, True, marks=pytest.mark.full),   # 2 chunks, 20 workgroups
     ],
 )
 def test_gdn_prefill_small(B, T, H, with_h0):
