@@ -1,9 +1,9 @@
 // Flash-attention forward for gfx950 (tileops_mha_fwd), BSHD layout.
 //
-// One workgroup = WAVES wavefronts (8 at launch: BM = 256 query rows of one
-// (batch, head)); each wavefront owns 32 query rows.  Keys/values stream
-// through LDS in tiles of BN = 64 rows, prefetched into registers one tile
-// ahead.
+// One workgroup = 8 wavefronts = BM = 256 query rows of one (batch, head);
+// each wavefront owns 32 query rows.  Keys/values stream through LDS in
+// tiles of BN = 64 rows, three LDS slots per operand, filled by
+// direct-to-LDS loads (no register staging) two tile steps ahead.
 //
 // Both products run on v_mfma_f32_32x32x16_{bf16,f16} in the *transposed*
 // orientation:
@@ -13,14 +13,20 @@
 // and 16 key rows of each 32-key block (the other 16 sit in lane l ^ 32).
 // The online softmax is therefore lane-local except for one exchange with
 // the partner lane, and P feeds the second MFMA straight from registers.
-// The summation order over keys inside a 16-key MFMA step is free, so V^T is
-// stored in LDS with each 16-key group permuted to match the key rows a lane
-// holds: the A operand of every step is then a single 16-byte LDS read.
+// V stays in LDS as loaded (key rows); its A operand comes from transpose
+// reads (ds_read_b64_tr_b16), which deliver one head dim of four
+// consecutive keys per lane in the key order P^T has in registers.
+//
+// The two groups of four wavefronts alternate between MFMA work and the
+// softmax (ping-pong), so that every SIMD, which hosts one wavefront of
+// each group, has MFMA work while the other wavefront computes exponentials.
 //
 // The softmax runs in the log2 domain (scores scaled by scale * log2 e); the
 // per-row LSE written out is m + log2(l), i.e. logsumexp(scale q k^T) / ln 2.
 #include <float.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 #include "common.h"
 
@@ -50,46 +56,104 @@ template <> struct Mfma<f16> {
 // fp32 / bf16) and the O accumulator is rescaled rarely.
 constexpr float kLazyLog2 = 8.0f;
 
-// position of key group `group4` (4 keys) inside an LDS row of V^T: within
-// each 16-key group the 4-key blocks are stored in the order 0, 2, 1, 3.
-__device__ __forceinline__ int vt_pos(int group4) {
-  const int j = group4 & 3;
-  const int pj = (j == 1) ? 2 : (j == 2 ? 1 : j);
-  return (group4 >> 2) * 16 + pj * 4;
-}
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-template <int D, int BN> struct Smem {
-  static constexpr int KS = D + 8;   // K row stride (elements): 16 B pad
-  static constexpr int VS = BN + 8;  // V^T row stride (elements): 16 B pad
-  static constexpr int K_ELEMS = BN * KS;
-  static constexpr int V_ELEMS = D * VS;
+// K and V tiles live in LDS unpadded, rows of D / 8 16-byte chunks, chunks
+// XOR-swizzled by row: K so that an MFMA operand read (16 consecutive key
+// rows, one chunk each) hits 16 distinct 16-byte bank groups, V so that the
+// transpose reads of a half-wavefront (4 consecutive key rows x 64 bytes)
+// cover all 64 banks once.
+template <int D> struct Swz {
+  static constexpr int CPR = D / 8;  // chunks per row
+  __device__ __forceinline__ static int k_key(int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); }
+  __device__ __forceinline__ static int v_key(int r) { return CPR == 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 };
 
-template <typename T, int D, bool CAUSAL, int WAVES, int BN>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void mha_fwd_kernel(
+// Workgroup barrier that waits only for this wavefront's LDS accesses, so
+// that direct-to-LDS loads issued before it stay in flight across it.  The
+// scheduling barriers keep arithmetic on its side as well: s_barrier alone
+// orders memory accesses, but MFMA or VALU work could otherwise drift into
+// the neighbouring phase, where the ping-pong has the other group's work.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One 16-byte direct-to-LDS load per lane: lane l reads 16 bytes at
+// `base + off` (base uniform, in SGPRs; off a per-lane byte offset) and they
+// land at LDS byte address lds + 16 l.  Issued as inline assembly so that the
+// compiler does not track the LDS write: every wait for these loads is
+// explicit (vmcnt) and followed by a workgroup barrier before any wavefront
+// reads the data.
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void_ptr)p;
+}
+
+// Per-lane source byte offsets of the tile gather: the four wavefronts of a
+// group take every fourth 1 KB window of a swizzled [BN][D] tile; lane l of
+// window `win` fills LDS chunk win * 64 + l, i.e. row r = (win * 64 + l) /
+// (D / 8), position p, with global chunk p ^ key(r) of key row min(r, rmax).
+template <typename T, int D, int BN, bool IS_V>
+__device__ __forceinline__ void gather_offsets(uint32_t (&off)[BN * D / 2048], int64_t stride,
+                                               int rmax, int gw, int lane) {
+  constexpr int CPR = D / 8;
+#pragma unroll
+  for (int i = 0; i < BN * D / 2048; ++i) {
+    const int win = 4 * i + gw;
+    const int ch = win * 64 + lane;
+    const int r = ch / CPR, p = ch % CPR;
+    const int key = IS_V ? Swz<D>::v_key(r) : Swz<D>::k_key(r);
+    off[i] = (uint32_t)(((int64_t)min(r, rmax) * stride + ((p ^ key) << 3)) * sizeof(T));
+  }
+}
+
+// Ping-pong schedule.  The 8 wavefronts form two groups, A = waves 0-3 and
+// B = waves 4-7, so that each SIMD hosts one wavefront of each.  A tile step
+// tau has two phases separated by workgroup barriers; in every phase one
+// group runs only MFMA work (O += V^T P^T of tile tau - 1, then S of tile
+// tau) while the other runs its softmax and issues direct-to-LDS loads:
+//   phase 0:  A: O(tau-1), S(tau)      B: softmax(tau-1), K(tau+2) -> slot
+//   phase 1:  A: softmax(tau), V(tau+1) -> slot      B: O(tau-1), S(tau)
+// K and V have three LDS slots each (tile t in slot t mod 3): within step tau
+// the groups read K(tau) and V(tau-1), the slots being filled held K(tau-1)
+// / V(tau-2), and every load has until the end of the next step to land
+// (each group ends its softmax phase waiting for everything but the windows
+// it just issued: vmcnt(4) for D = 128, vmcnt(2) for D = 64, vmcnt(0) when
+// it issued none).
+template <typename T, int D, bool CAUSAL, int BN>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void mha_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
     float* __restrict__ lse, int B, int Sq, int Skv, int H, int Hkv, float scale_log2, int nqb) {
   typedef typename Mfma<T>::V8 V8;
-  typedef Smem<D, BN> SM;
-  constexpr int NKB = BN / 32;           // 32-key blocks per tile
-  constexpr int kThreads = WAVES * 64;
-  constexpr int BM = WAVES * 32;         // query rows per workgroup
-  constexpr int KSTEPS = D / 16;         // MFMA steps over the head dim
-  constexpr int DBLK = D / 32;           // 32-row blocks of O^T
-  constexpr int KCHUNK = D / 8;          // 16-byte chunks per K row
-  constexpr int KLOADS = BN * KCHUNK / kThreads;  // 16-byte K loads per thread
-  constexpr int VGROUPS = (BN / 4) * (D / 8);     // (4 keys x 8 dims) units
-  static_assert(KLOADS * kThreads == BN * KCHUNK, "K tile must split evenly over threads");
-  static_assert(VGROUPS <= kThreads, "one V unit per thread at most");
+  constexpr int NKB = BN / 32;    // 32-key blocks per tile
+  constexpr int BM = 256;         // query rows per workgroup (8 x 32)
+  constexpr int KSTEPS = D / 16;  // MFMA steps over the head dim
+  constexpr int DBLK = D / 32;    // 32-row blocks of O^T
+  constexpr int TILE = BN * D;    // elements per K or V tile
+  constexpr int WPW = TILE / 512 / 4;  // 1 KB load windows per wavefront per tile
+  static_assert(BN == 64, "the schedule assumes 64-key tiles");
+  static_assert(WPW >= 1 && WPW <= 15, "vmcnt immediate");
 
-  __shared__ __attribute__((aligned(16))) T k_lds[SM::K_ELEMS];
-  __shared__ __attribute__((aligned(16))) T v_lds[SM::V_ELEMS];
+  __shared__ __attribute__((aligned(16))) T k_lds[3 * TILE];
+  __shared__ __attribute__((aligned(16))) T v_lds[3 * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront-uniform
   const int col = lane & 31;  // query row inside the wave's 32
   const int half = lane >> 5;
+  const bool grp_a = wave < 4;
+  const int gw = wave & 3;     // wavefront index inside its group
 
   // --- XCD-aware block order: workgroups are dealt round-robin to the 8
   // XCDs; regroup so that one XCD works through all query blocks of a head
@@ -125,90 +189,159 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2
   }
 
   const int kv_end = CAUSAL ? min(Skv, q0 + BM + off) : Skv;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
-  // --- register prefetch of one K / V tile
-  u32x4 kpre[KLOADS];
-  u32x4 vpre[4];
-  constexpr int NG = BN / 4;    // 4-key groups per tile
-  const bool v_owner = tid < VGROUPS;
-  const int vg = tid % NG;      // 4-key group
-  const int vc = tid / NG;      // 8-dim chunk
-  auto prefetch = [&](int tile) {
-    const int kv0 = tile * BN;
+  // Gather offsets of this wavefront's windows (group B loads K, group A
+  // loads V); the last tile, if ragged, uses offsets with its rows clamped
+  // to the last key row (their scores are masked to -inf).  Tiles past the
+  // last one are not loaded, so every row index stays in [0, Skv).
+  constexpr int NW = BN * D / 2048;  // windows per wavefront per tile (== WPW)
+  static_assert(NW == WPW, "window count");
+  uint32_t goff[NW];
+  if (grp_a)
+    gather_offsets<T, D, BN, true>(goff, kv_row, BN - 1, gw, lane);
+  else
+    gather_offsets<T, D, BN, false>(goff, kv_row, BN - 1, gw, lane);
+  const T* gsrc = grp_a ? vbase : kbase;
+  T* gdst = grp_a ? v_lds : k_lds;
+  auto load_tile = [&](int t) __device__ __attribute__((always_inline)) {
+    if (t >= ntiles) return;
+    const T* src = gsrc + (int64_t)t * BN * kv_row;
+    const uint32_t lds = lds_addr(gdst + (uint32_t)(t % 3) * TILE) + (uint32_t)gw * 1024;
+    if (t * BN + BN <= Skv) {
 #pragma unroll
-    for (int i = 0; i < KLOADS; ++i) {
-      const int c = tid + i * kThreads;
-      const int r = c / KCHUNK, cc = c % KCHUNK;
-      const int kv = kv0 + r;
-      kpre[i] = kv < Skv ? *reinterpret_cast<const u32x4*>(kbase + (int64_t)kv * kv_row + cc * 8)
-                         : u32x4{0, 0, 0, 0};
-    }
-    if (v_owner) {
+      for (int i = 0; i < NW; ++i) lds_dma16(src, goff[i], lds + i * 4096);
+    } else {
+      uint32_t c[NW];
+      if (grp_a)
+        gather_offsets<T, D, BN, true>(c, kv_row, Skv - 1 - t * BN, gw, lane);
+      else
+        gather_offsets<T, D, BN, false>(c, kv_row, Skv - 1 - t * BN, gw, lane);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kv = kv0 + vg * 4 + i;
-        vpre[i] = kv < Skv ? *reinterpret_cast<const u32x4*>(vbase + (int64_t)kv * kv_row + vc * 8)
-                           : u32x4{0, 0, 0, 0};
-      }
+      for (int i = 0; i < NW; ++i) lds_dma16(src, c[i], lds + i * 4096);
     }
   };
-  auto commit = [&]() {
-#pragma unroll
-    for (int i = 0; i < KLOADS; ++i) {
-      const int c = tid + i * kThreads;
-      const int r = c / KCHUNK, cc = c % KCHUNK;
-      *reinterpret_cast<u32x4*>(k_lds + r * SM::KS + cc * 8) = kpre[i];
-    }
-    if (v_owner) {
-      // transpose 4 keys x 8 dims: dim d gets the 4 keys as one 8-byte write
-      const int pos = vt_pos(vg);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {  // dword m of each row = dims 2m, 2m+1
-        const uint32_t a0 = vpre[0][m], a1 = vpre[1][m], a2 = vpre[2][m], a3 = vpre[3][m];
-        // low halves -> dim 2m, high halves -> dim 2m + 1
-        const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
-        const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
-        const uint32_t hi01 = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
-        const uint32_t hi23 = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-        const int d = vc * 8 + 2 * m;
-        *reinterpret_cast<uint2*>(v_lds + d * SM::VS + pos) = make_uint2(lo01, lo23);
-        *reinterpret_cast<uint2*>(v_lds + (d + 1) * SM::VS + pos) = make_uint2(hi01, hi23);
-      }
-    }
+  // End of a softmax phase: every tile this wavefront loaded earlier has
+  // landed (the other group reads it after the next barrier); the WPW
+  // windows of tile t, issued in this phase if t exists, may stay in flight.
+  auto wait_loads = [&](int t) __device__ __attribute__((always_inline)) {
+    if (t < ntiles)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | WPW);  // vmcnt(WPW)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   };
 
   f32x16 acc_o[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) acc_o[i] = f32x16{};
+  f32x16 acc_s[NKB];
+  V8 pb[2 * NKB];
   float m_run = -INFINITY;  // running max of raw scores (q . k)
   float l_run = 0.0f;
   const float lazy_raw = kLazyLog2 / scale_log2;
 
-  if (ntiles > 0) prefetch(0);
-  for (int t = 0; t < ntiles; ++t) {
-    if (t > 0) __syncthreads();  // every wave is done reading the last tile
-    commit();
-    __syncthreads();
-    if (t + 1 < ntiles) prefetch(t + 1);
-    const int kv0 = t * BN;
+  // Lane-dependent element offsets of the operand reads (the slot base is
+  // added per read).
+  // K (S^T A operand): row kb * 32 + col, chunk 2 ks + half, swizzled; the kb
+  // term is a constant added at the read.
+  int koff[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks)
+    koff[ks] = col * D + (((ks * 2 + half) ^ Swz<D>::k_key(col)) << 3);
+  // V^T (O^T A operand) through transpose reads: in each group of 16 lanes,
+  // lane j points at 4 dims (4 (j % 4) ..) of key row j / 4 and receives
+  // dim j of those 4 keys.  Key slot 4 rr + e of lane half g is key
+  // 16 ks + 8 rr + 4 g + e, the order in which P^T sits in registers; the
+  // ks and rr terms are constants (the swizzle key depends on row % 4 only).
+  const int grp16 = lane >> 4, j16 = lane & 15;
+  const int vrow = 4 * (grp16 >> 1) + (j16 >> 2);
+  int voff[DBLK];
+#pragma unroll
+  for (int db = 0; db < DBLK; ++db) {
+    const int dim = db * 32 + 16 * (grp16 & 1) + 4 * (j16 & 3);
+    voff[db] = vrow * D + ((((dim >> 3) ^ Swz<D>::v_key(vrow)) << 3) | (dim & 7));
+  }
 
-    // S^T = K . Q^T : NKB 32-key blocks, their MFMA chains interleaved
-    f32x16 acc_s[NKB];
+  // Operand reads: `vb` / `kb` are the LDS byte addresses of this lane's
+  // first V^T / K element in the current slots, re-derived at the start of
+  // each MFMA phase and made opaque, so that the per-read constants (key
+  // and head-dim steps) become DS immediate offsets rather than one address
+  // computation per read.
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  typedef __attribute__((address_space(3))) V8 lds_v8;
+  // A operand of the O^T update: 8 keys (16 ks + 8 rr + ..) of dim block db,
+  // two 64-bit transpose reads assembled by whole-register moves
+  auto read_vt = [&](uint32_t vb, int ks) __device__ __attribute__((always_inline)) -> V8 {
+    const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks) * D * 2));
+    const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks + 8) * D * 2));
+    const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
+    const u32x4 w = {y0.x, y0.y, y1.x, y1.y};
+    return __builtin_bit_cast(V8, w);
+  };
+  auto read_k = [&](uint32_t kb, int blk) __device__ __attribute__((always_inline)) -> V8 {
+    return *(lds_v8*)(uintptr_t)(kb + blk * 32 * D * 2);
+  };
+
+  // The MFMA phase as one sequence: per 16-key step j, the DBLK O^T blocks
+  // of keys 16 j .. 16 j + 15 (when DO_O), then the S^T products of head-dim
+  // steps KS4 j .. KS4 j + KS4 - 1 for both 32-key blocks (when DO_S), so
+  // that up to DBLK + 2 independent accumulators alternate; each operand is
+  // read from LDS two MFMAs ahead into a ring of three register sets.
+  auto mfma_phase = [&](auto do_o, auto do_s, const T* vl, const T* kl)
+      __device__ __attribute__((always_inline)) {
+    constexpr bool DO_O = decltype(do_o)::value, DO_S = decltype(do_s)::value;
+    constexpr int KS4 = KSTEPS / 4;                        // head-dim steps per 16-key step
+    constexpr int WO = DO_O ? DBLK : 0, WS = DO_S ? KS4 * NKB : 0;
+    constexpr int W = WO + WS;                             // MFMAs per 16-key step
+    constexpr int N = 4 * W;
+    static_assert(BN / 16 == 4 && KSTEPS % 4 == 0, "four 16-key steps per tile");
+    if (DO_S) {
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) acc_s[kb] = f32x16{};
+      for (int kb = 0; kb < NKB; ++kb) acc_s[kb] = f32x16{};
+    }
+    uint32_t vb[DBLK], kb[KSTEPS];
+    const uint32_t vl_addr = lds_addr(vl), kl_addr = lds_addr(kl);
+    if (DO_O) {
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        const V8 a =
-            *reinterpret_cast<const V8*>(k_lds + (kb * 32 + col) * SM::KS + ks * 16 + half * 8);
-        acc_s[kb] = Mfma<T>::run(a, qreg[ks], acc_s[kb]);
+      for (int db = 0; db < DBLK; ++db) {
+        vb[db] = vl_addr + voff[db] * 2;
+        asm volatile("" : "+v"(vb[db]));
       }
     }
+    if (DO_S) {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        kb[ks] = kl_addr + koff[ks] * 2;
+        asm volatile("" : "+v"(kb[ks]));
+      }
+    }
+    auto fetch = [&](int n) __device__ __attribute__((always_inline)) -> V8 {
+      const int j = n / W, w = n % W;
+      if (w < WO) return read_vt(vb[w], j);
+      return read_k(kb[KS4 * j + (w - WO) / NKB], (w - WO) % NKB);
+    };
+    V8 ring[3];
+    ring[0] = fetch(0);
+    ring[1] = fetch(1);
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      if (n + 2 < N) ring[(n + 2) % 3] = fetch(n + 2);
+      const int j = n / W, w = n % W;
+      if (w < WO) {
+        acc_o[w] = Mfma<T>::run(ring[n % 3], pb[j], acc_o[w]);
+      } else {
+        const int ks = KS4 * j + (w - WO) / NKB, kb = (w - WO) % NKB;
+        acc_s[kb] = Mfma<T>::run(ring[n % 3], qreg[ks], acc_s[kb]);
+      }
+    }
+  };
+  typedef std::integral_constant<bool, true> yes;
+  typedef std::integral_constant<bool, false> no;
 
-    // online softmax for query row qi: maxima in raw score units, the scale
-    // (times log2 e) folded into one FMA per score inside exp2
+  // online softmax of tile t for query row qi: maxima in raw score units,
+  // the scale (times log2 e) folded into one FMA per score inside exp2
+  auto softmax = [&](int t) __device__ __attribute__((always_inline)) {
+    const int kv0 = t * BN;
     // masking only on the ragged last tile and on causal diagonal tiles
     // (a workgroup-uniform branch, kept out of the common path)
     if ((kv0 + BN > Skv) || (CAUSAL && kv0 + BN - 1 > q0 + off)) {
@@ -222,12 +355,14 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2
         }
       }
     }
-    float tmax = -INFINITY;
+    // four independent max / sum chains (fp32 max is exact in any order)
+    float tm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, acc_s[kb][r]);
+      for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], acc_s[kb][r]);
     }
+    float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const bool grow = tmax > m_run + lazy_raw;
     if (__any(grow)) {
@@ -244,8 +379,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2
     }
     // rows with no visible key yet keep m = -inf: shift by 0 so exp2 -> 0
     const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * scale_log2;
-    float psum = 0.0f;
-    V8 pb[2 * NKB];
+    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
@@ -253,23 +387,75 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2
         // fp32 probabilities form the row sum (and the LSE); P is rounded to
         // the storage type only as the MFMA operand
         const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[kb][r], scale_log2, neg_mc));
-        psum += p;
+        ps[r & 3] += p;
         pb[kb * 2 + (r >> 3)][r & 7] = (T)p;
       }
     }
-    l_run += psum;
+    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    // materialise P here: pure arithmetic may otherwise sink past the next
+    // barrier into the O update, out of the phase meant to overlap the
+    // other group's MFMA work
+#pragma unroll
+    for (int i = 0; i < 2 * NKB; ++i) asm volatile("" : "+v"(pb[i]));
+    asm volatile("" : "+v"(l_run));
+  };
 
-    // O^T += V^T . P^T (independent d-blocks interleaved)
-#pragma unroll
-    for (int ks = 0; ks < BN / 16; ++ks) {
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db) {
-        const V8 a =
-            *reinterpret_cast<const V8*>(v_lds + (db * 32 + col) * SM::VS + ks * 16 + half * 8);
-        acc_o[db] = Mfma<T>::run(a, pb[ks], acc_o[db]);
-      }
+  // --- prologue: K(0), K(1) (group B) and V(0) (group A) into their slots
+  load_tile(0);
+  if (!grp_a) load_tile(1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  // One loop per group, each body a softmax phase then an MFMA phase (group
+  // A's steps rotated by half a step so that both loops have that shape);
+  // both pass 2 (ntiles + 1) barriers in all.
+  //   A, tau:  softmax(tau), V(tau+1) | O(tau), S(tau+1)
+  //   B, tau:  softmax(tau-1), K(tau+2) | O(tau-1), S(tau)
+  // The last step of each loop (O only, no S) is peeled off, so that the
+  // loop body holds a single MFMA sequence.
+  if (grp_a) {
+    if (ntiles > 0) mfma_phase(no(), yes(), v_lds, k_lds);  // S(0)
+    lds_barrier();
+    for (int tau = 0; tau + 1 < ntiles; ++tau) {
+      load_tile(tau + 1);
+      softmax(tau);
+      wait_loads(tau + 1);
+      lds_barrier();
+      mfma_phase(yes(), yes(), v_lds + (tau % 3) * TILE, k_lds + ((tau + 1) % 3) * TILE);
+      lds_barrier();
+    }
+    if (ntiles > 0) {
+      const int tau = ntiles - 1;
+      softmax(tau);
+      wait_loads(ntiles);
+      lds_barrier();
+      mfma_phase(yes(), no(), v_lds + (tau % 3) * TILE, k_lds);
+      lds_barrier();
+    }
+    lds_barrier();  // softmax phase of step ntiles (nothing left to do)
+  } else {
+    load_tile(2);
+    wait_loads(2);
+    lds_barrier();
+    if (ntiles > 0) mfma_phase(no(), yes(), v_lds, k_lds);  // S(0)
+    lds_barrier();
+    for (int tau = 1; tau < ntiles; ++tau) {
+      load_tile(tau + 2);
+      softmax(tau - 1);
+      wait_loads(tau + 2);
+      lds_barrier();
+      mfma_phase(yes(), yes(), v_lds + ((tau - 1) % 3) * TILE, k_lds + (tau % 3) * TILE);
+      lds_barrier();
+    }
+    if (ntiles > 0) {
+      const int tau = ntiles;
+      softmax(tau - 1);
+      wait_loads(ntiles);
+      lds_barrier();
+      mfma_phase(yes(), no(), v_lds + ((tau - 1) % 3) * TILE, k_lds);
+      lds_barrier();
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // no load may land after the workgroup's LDS is released
 
   // --- epilogue: combine the two half-row sums, normalise, store
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -293,20 +479,20 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2
   }
 }
 
-template <typename T, int D, int WAVES, int BN>
+template <typename T, int D, int BN>
 static int launch(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Sq,
                   int Skv, int H, int Hkv, bool causal, float scale, hipStream_t s) {
-  constexpr int BM = WAVES * 32;
+  constexpr int BM = 256;
   const int nqb = (Sq + BM - 1) / BM;
   const int64_t total = (int64_t)nqb * H * B;
   const float scale_log2 = scale * 1.4426950408889634f;
-  dim3 grid((unsigned)total), block(WAVES * 64);
+  dim3 grid((unsigned)total), block(512);
   if (causal)
-    mha_fwd_kernel<T, D, true, WAVES, BN><<<grid, block, 0, s>>>(
+    mha_fwd_kernel<T, D, true, BN><<<grid, block, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
         static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, scale_log2, nqb);
   else
-    mha_fwd_kernel<T, D, false, WAVES, BN><<<grid, block, 0, s>>>(
+    mha_fwd_kernel<T, D, false, BN><<<grid, block, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
         static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, scale_log2, nqb);
   return launch_status();
@@ -315,10 +501,7 @@ static int launch(const void* q, const void* k, const void* v, void* o, float* l
 template <typename T, int D>
 static int launch_w(const void* q, const void* k, const void* v, void* o, float* lse, int B,
                     int Sq, int Skv, int H, int Hkv, bool causal, float scale, hipStream_t s) {
-  // 8 wavefronts x 32 query rows, 64-key tiles: measured best on MI355X
-  // among 4 / 8 wavefronts and 64 / 128-key tiles, and among software-
-  // pipelined variants with Q in LDS and double-buffered K / V slots.
-  return launch<T, D, 8, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
+  return launch<T, D, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
 }
 
 template <typename T>
