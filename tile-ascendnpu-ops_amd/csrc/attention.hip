@@ -99,6 +99,20 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_void_ptr)p;
 }
 
+// Combine a value with the one held by the partner lane l ^ 32 (VALU lane
+// swap between the two wavefront halves, no LDS round trip): the two
+// outputs of v_permlane32_swap on (x, x) are x's low and high halves.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, x), false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+
 // Per-lane source byte offsets of the tile gather: the four wavefronts of a
 // group take every fourth 1 KB window of a swizzled [BN][D] tile; lane l of
 // window `win` fills LDS chunk win * 64 + l, i.e. row r = (win * 64 + l) /
@@ -286,7 +300,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // of keys 16 j .. 16 j + 15 (when DO_O), then the S^T products of head-dim
   // steps KS4 j .. KS4 j + KS4 - 1 for both 32-key blocks (when DO_S), so
   // that up to DBLK + 2 independent accumulators alternate; each operand is
-  // read from LDS two MFMAs ahead into a ring of three register sets.
+  // read from LDS PF MFMAs ahead into a ring of PF + 1 register sets.
   auto mfma_phase = [&](auto do_o, auto do_s, const T* vl, const T* kl)
       __device__ __attribute__((always_inline)) {
     constexpr bool DO_O = decltype(do_o)::value, DO_S = decltype(do_s)::value;
@@ -320,18 +334,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (w < WO) return read_vt(vb[w], j);
       return read_k(kb[KS4 * j + (w - WO) / NKB], (w - WO) % NKB);
     };
-    V8 ring[3];
-    ring[0] = fetch(0);
-    ring[1] = fetch(1);
+    constexpr int PF = 3;  // operand reads in flight ahead of the MFMA using them
+    V8 ring[PF + 1];
+#pragma unroll
+    for (int n = 0; n < PF; ++n) ring[n] = fetch(n);
 #pragma unroll
     for (int n = 0; n < N; ++n) {
-      if (n + 2 < N) ring[(n + 2) % 3] = fetch(n + 2);
+      if (n + PF < N) ring[(n + PF) % (PF + 1)] = fetch(n + PF);
       const int j = n / W, w = n % W;
       if (w < WO) {
-        acc_o[w] = Mfma<T>::run(ring[n % 3], pb[j], acc_o[w]);
+        acc_o[w] = Mfma<T>::run(ring[n % (PF + 1)], pb[j], acc_o[w]);
       } else {
         const int ks = KS4 * j + (w - WO) / NKB, kb = (w - WO) % NKB;
-        acc_s[kb] = Mfma<T>::run(ring[n % 3], qreg[ks], acc_s[kb]);
+        acc_s[kb] = Mfma<T>::run(ring[n % (PF + 1)], qreg[ks], acc_s[kb]);
       }
     }
   };
@@ -363,7 +378,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], acc_s[kb][r]);
     }
     float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = pair_max(tmax);
     const bool grow = tmax > m_run + lazy_raw;
     if (__any(grow)) {
       const float m_new = grow ? tmax : m_run;
@@ -458,7 +473,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __builtin_amdgcn_s_waitcnt(0);  // no load may land after the workgroup's LDS is released
 
   // --- epilogue: combine the two half-row sums, normalise, store
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = pair_sum(l_run);
   const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (qi < Sq) {
     T* orow = o + ((int64_t)bb * Sq + qi) * q_row + (int64_t)hq * D;
