@@ -81,6 +81,19 @@ __device__ __forceinline__ void store_transposed4x8(bf16* dst, int stride, int d
   }
 }
 
+// Workgroup barrier that waits only for this wavefront's LDS accesses
+// (lgkmcnt(0); vmcnt and expcnt left at their maxima), so that global loads
+// and stores issued before it stay in flight across it (direct-to-LDS loads
+// included).  __syncthreads() would also wait for them: its fence drains
+// every outstanding memory access.  Only LDS data is exchanged through these
+// barriers; register results of global loads are waited for at their use.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // kernel 1: per-chunk preparation
 // ---------------------------------------------------------------------------
@@ -190,7 +203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       fac_ws[lane] = scale * exp2f_fast(x * kLog2e);
       if (lane < kFacN - C) fac_ws[C + lane] = lane == 0 ? exp2f_fast(gl * kLog2e) : 0.0f;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- K K^T -> A^T (fp32, LDS) and Q K^T -> Aqk (bf16, LDS), in 32x32
     // blocks (row block rb, column block cb).  Only the strictly lower parts of
@@ -228,7 +241,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int r = 0; r < 16; ++r) aqk_s[((r >> 2) * 8 + half * 4 + (r & 3)) * CP + cs] = (bf16)0.0f;
     }
     if (blk + gridDim.x < nblk) load(blk + gridDim.x, cur);  // operands consumed: next chunk
-    __syncthreads();
+    lds_barrier();
 
     // ---- Aqk rows to the workspace (16-byte stores); T = (I + A)^-1, blocked
     // by 16: the four diagonal blocks Tbb by substitution (wave w: block w,
@@ -271,7 +284,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     // v_mfma_f32_16x16x4f32 lanes: A[mi][mk], B[mk][mi], D[4 mk + r][mi]
     const int mi = lane & 15, mk = lane >> 4;
     if (wave < 2) {  // Y = A10 T00 (wave 0) / A32 T22 (wave 1) -> x_s rows 16 wave ..
@@ -286,7 +299,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int r = 0; r < 4; ++r) x_s[(16 * wave + 4 * mk + r) * XS + mi] = y[r];
     }
-    __syncthreads();
+    lds_barrier();
     if (wave < 2) {  // T10 = -T11 Y (wave 0), T32 = -T33 Y (wave 1)
       const int d0 = 32 * wave;
       f32x4 z = {};
@@ -303,7 +316,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int r = 0; r < 4; ++r) t_s[(d0 + 4 * mk + r) * AS + d0 + 16 + mi] = 0.0f;
     }
-    __syncthreads();
+    lds_barrier();
     const int qi = wave >> 1, qj = wave & 1;  // 16x16 quadrant of a 32x32 block
     {  // X = A21 T11 -> x_s
       f32x4 x = {};
@@ -316,7 +329,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int r = 0; r < 4; ++r) x_s[(16 * qi + 4 * mk + r) * XS + 16 * qj + mi] = x[r];
     }
-    __syncthreads();
+    lds_barrier();
     {  // T21 = -T22 X
       f32x4 y = {};
 #pragma unroll
@@ -328,7 +341,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int r = 0; r < 4; ++r) t_s[(32 + 16 * qi + 4 * mk + r) * AS + 16 * qj + mi] = -y[r];
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- Tw = T diag(beta exp(gc)), Tu = T diag(beta) in bf16 (T12 is zero)
     // (4 consecutive columns per thread: float4 in, 8-byte bf16 stores out)
@@ -344,7 +357,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       *reinterpret_cast<uint2*>(tw_s + i * CP + j) = *reinterpret_cast<uint2*>(pw);
       *reinterpret_cast<uint2*>(tu_s + i * CP + j) = *reinterpret_cast<uint2*>(pu);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- Tu rows to the workspace; -w^T = -(k^T Tw^T): wave -> 32-row block of
     // d; the accumulator holds 4 consecutive d of one token row l (8 bytes)
@@ -392,7 +405,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       o8[6] = (bf16)((float)kv[6] * f1.z); o8[7] = (bf16)((float)kv[7] * f1.w);
       *reinterpret_cast<bf16x8*>(kd_ws + d * C + c8) = o8;
     }
-    __syncthreads();  // LDS is rewritten by the next chunk
+    lds_barrier();  // LDS is rewritten by the next chunk
   }
 }
 
@@ -420,17 +433,6 @@ __device__ __forceinline__ int swz16(int r, int kc) { return r * DK + ((kc ^ (r 
 __device__ __forceinline__ int swz8(int r, int kc) { return r * C + ((kc ^ ((r >> 1) & 7)) << 3); }
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
-// Workgroup barrier that waits only for this wavefront's LDS accesses
-// (lgkmcnt(0); vmcnt and expcnt left at their maxima), so that direct-to-LDS
-// loads issued before it stay in flight across it.  __syncthreads() would
-// also wait for them.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // Fill the swizzled image `dst` (NCH 16-byte chunks, CPR per row) from the
 // rows `src + min(r, rmax) * stride` (elements).  Each of the 4 wavefronts
