@@ -360,13 +360,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     lds_barrier();
 
     // ---- Tu rows to the workspace; -w^T = -(k^T Tw^T): wave -> 32-row block of
-    // d; the accumulator holds 4 consecutive d of one token row l (8 bytes)
+    // d; the accumulator holds 4 consecutive d of one token row l (8 bytes),
+    // staged in the dead T region as [C][KP] bf16 so that the workspace rows
+    // are then written in whole 16-byte chunks (16 lanes per 256-byte row)
 #pragma unroll
     for (int e = tid; e < C * C / 8; e += 256) {
       const int row = e >> 3, c8 = (e & 7) * 8;
       *reinterpret_cast<u32x4*>(tu_ws + row * C + c8) =
           *reinterpret_cast<const u32x4*>(tu_s + row * CP + c8);
     }
+    bf16* w_s = reinterpret_cast<bf16*>(r0);  // T is dead after the Tw / Tu conversion
     {
       const int db = wave;
 #pragma unroll
@@ -385,7 +388,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
           for (int e = 0; e < 4; ++e) pw[e] = (bf16)(-aw[g4 * 4 + e]);
           const int d = db * 32 + g4 * 8 + half * 4;
-          *reinterpret_cast<uint2*>(w_ws + l * DK + d) = *reinterpret_cast<uint2*>(pw);
+          *reinterpret_cast<uint2*>(w_s + l * KP + d) = *reinterpret_cast<uint2*>(pw);
         }
       }
     }
@@ -404,6 +407,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       o8[4] = (bf16)((float)kv[4] * f1.x); o8[5] = (bf16)((float)kv[5] * f1.y);
       o8[6] = (bf16)((float)kv[6] * f1.z); o8[7] = (bf16)((float)kv[7] * f1.w);
       *reinterpret_cast<bf16x8*>(kd_ws + d * C + c8) = o8;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < C * DK / 8 / 256; ++j) {  // -w rows, [C][DK]
+      const int e = tid + 256 * j;
+      const int row = e >> 4, c8 = (e & 15) * 8;
+      *reinterpret_cast<u32x4*>(w_ws + row * DK + c8) =
+          *reinterpret_cast<const u32x4*>(w_s + row * KP + c8);
     }
     lds_barrier();  // LDS is rewritten by the next chunk
   }
