@@ -64,3 +64,9 @@ def test_host_side_argument_rejection(lib):
     assert lib.tileops_argreduce_fwd(None, None, 0, 8, 0, 0, None) == 0
     assert lib.tileops_fused_add_layernorm_fwd(None, None, None, None, None, None, 4, 8, 1e-5,
                                                2, 1, None) == -1  # fp16 params for bf16 x
+    # causal attention with more queries than keys (the right-aligned mask
+    # would leave whole query blocks without a key) is rejected, as the Op does
+    assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 333, 200, 2, 2, 128, 1, 1.0,
+                               2, None) == -2
+    assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 333, 200, 2, 2, 128, 0, 1.0,
+                               2, None) == -3  # non-causal: fine until the null pointers
