@@ -63,6 +63,29 @@ __device__ __forceinline__ bf16x8 ld8(const bf16* p) {  // 16-byte load (LDS or 
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Inclusive prefix sum over the 64 lanes of a wavefront by DPP lane moves,
+// with no LDS round trip (a shuffle-based scan waits on the LDS queue, which
+// the other workgroup of the CU keeps busy): Hillis-Steele inside each row
+// of 16 lanes (row_shr 1, 2, 4, 8; lanes shifted in from outside the row
+// read 0), then each row's total carried forward: row_bcast:15 adds lane
+// 16 r + 15 to row r + 1 (rows 1 and 3), row_bcast:31 adds lane 31 to rows
+// 2 and 3.
+__device__ __forceinline__ float dpp_add(float x, int moved) {
+  return x + __builtin_bit_cast(float, moved);
+}
+__device__ __forceinline__ float wave_inclusive_sum(float x) {
+#define TILEOPS_DPP(ctrl, rows) \
+  __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), ctrl, rows, 0xF, true)
+  x = dpp_add(x, TILEOPS_DPP(0x111, 0xF));  // row_shr:1
+  x = dpp_add(x, TILEOPS_DPP(0x112, 0xF));  // row_shr:2
+  x = dpp_add(x, TILEOPS_DPP(0x114, 0xF));  // row_shr:4
+  x = dpp_add(x, TILEOPS_DPP(0x118, 0xF));  // row_shr:8
+  x = dpp_add(x, TILEOPS_DPP(0x142, 0xA));  // row_bcast:15 -> rows 1, 3
+  x = dpp_add(x, TILEOPS_DPP(0x143, 0xC));  // row_bcast:31 -> rows 2, 3
+#undef TILEOPS_DPP
+  return x;
+}
+
 // Store a 4-row x 8-column tile (4 packs of 8 bf16, one per row) transposed
 // into an LDS array with row stride `stride`: column d gets the 4 rows as one
 // 8-byte write at [d][r0].
@@ -188,17 +211,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (wave == 0) {
       float x = lane < n ? cur.g : 0.0f;
       const float bt = lane < n ? cur.beta : 0.0f;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {  // inclusive prefix sum over the chunk
-        const float y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-      }
+      x = wave_inclusive_sum(x);  // gc: inclusive prefix sum over the chunk
       gc_s[lane] = x;
       beta_s[lane] = bt;
       be_s[lane] = bt * exp2f_fast(x * kLog2e);
       // factors the recurrence applies: scale e^{gc} per output row, the
       // chunk decay e^{gc_C}, and e^{gc_C - gc} for the decayed keys
-      const float gl = __shfl(x, C - 1, 64);
+      const float gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), C - 1));
       dec_s[lane] = exp2f_fast((gl - x) * kLog2e);
       fac_ws[lane] = scale * exp2f_fast(x * kLog2e);
       if (lane < kFacN - C) fac_ws[C + lane] = lane == 0 ? exp2f_fast(gl * kLog2e) : 0.0f;
@@ -223,16 +242,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const float gcs = gc_s[cs];
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
+        const int cl0 = rb * 32 + g4 * 8 + half * 4;
+        const float4 gl4 = *reinterpret_cast<const float4*>(gc_s + cl0);
+        const float4 bl4 = *reinterpret_cast<const float4*>(beta_s + cl0);
+        const float glv[4] = {gl4.x, gl4.y, gl4.z, gl4.w}, blv[4] = {bl4.x, bl4.y, bl4.z, bl4.w};
         float a4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = g4 * 4 + e;
-          const int cl = rb * 32 + g4 * 8 + half * 4 + e;
-          const float gd = cl >= cs ? exp2f_fast((gc_s[cl] - gcs) * kLog2e) : 0.0f;
-          a4[e] = cl > cs ? beta_s[cl] * gd * kk[r] : 0.0f;
+          const int cl = cl0 + e;
+          // branch-free: the decay is evaluated for every element (its
+          // argument clamped to <= 0, exact where it is used) and then
+          // selected, so that no exec-masked branch surrounds each exp
+          float gd = exp2f_fast(fminf((glv[e] - gcs) * kLog2e, 0.0f));
+          asm volatile("" : "+v"(gd));
+          gd = cl >= cs ? gd : 0.0f;
+          a4[e] = cl > cs ? blv[e] * gd * kk[r] : 0.0f;
           aqk_s[cl * CP + cs] = (bf16)(scale * gd * qk[r]);
         }
-        const int cl0 = rb * 32 + g4 * 8 + half * 4;
         *reinterpret_cast<float4*>(at_s + cs * AS + cl0) = make_float4(a4[0], a4[1], a4[2], a4[3]);
       }
     } else {
