@@ -228,44 +228,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // blocks (row block rb, column block cb).  Only the strictly lower parts of
     // the diagonal blocks and the block A21 of A are ever read back.
     if (wave < 3) {
+      // transposed orientation: k rows s of block cb as the A operand, k / q
+      // rows l of block rb as B, so that a lane owns one row l (column of the
+      // result) and its 16 values run over s: [s][l] = k_s . k_l and k_s . q_l
       f32x16 kk = {}, qk = {};
       const bool qlive = qrow < n;
 #pragma unroll
       for (int ks = 0; ks < DK / 16; ++ks) {
-        const bf16x8 bk = ld8(k_s + (cb * 32 + col) * KP + ks * 16 + half * 8);
-        const bf16x8 ak = ld8(k_s + (rb * 32 + col) * KP + ks * 16 + half * 8);
+        const bf16x8 bs = ld8(k_s + (cb * 32 + col) * KP + ks * 16 + half * 8);
+        const bf16x8 bl = ld8(k_s + (rb * 32 + col) * KP + ks * 16 + half * 8);
         const bf16x8 a = qlive ? cur.aq[ks] : bf16x8{};
-        kk = mfma(ak, bk, kk);
-        qk = mfma(a, bk, qk);
+        kk = mfma(bs, bl, kk);
+        qk = mfma(bs, a, qk);
       }
-      const int cs = cb * 32 + col;
-      const float gcs = gc_s[cs];
+      const int l = rb * 32 + col;
+      const float gl = gc_s[l], bel = beta_s[l];
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        const int cl0 = rb * 32 + g4 * 8 + half * 4;
-        const float4 gl4 = *reinterpret_cast<const float4*>(gc_s + cl0);
-        const float4 bl4 = *reinterpret_cast<const float4*>(beta_s + cl0);
-        const float glv[4] = {gl4.x, gl4.y, gl4.z, gl4.w}, blv[4] = {bl4.x, bl4.y, bl4.z, bl4.w};
-        float a4[4];
+        const int s0 = cb * 32 + g4 * 8 + half * 4;
+        const float4 gs4 = *reinterpret_cast<const float4*>(gc_s + s0);
+        const float gsv[4] = {gs4.x, gs4.y, gs4.z, gs4.w};
+        bf16 q4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = g4 * 4 + e;
-          const int cl = cl0 + e;
+          const int sc = s0 + e;
           // branch-free: the decay is evaluated for every element (its
-          // argument clamped to <= 0, exact where it is used) and then
-          // selected, so that no exec-masked branch surrounds each exp
-          float gd = exp2f_fast(fminf((glv[e] - gcs) * kLog2e, 0.0f));
+          // argument clamped to <= 0, exact where it is used) and selected
+          float gd = exp2f_fast(fminf((gl - gsv[e]) * kLog2e, 0.0f));
           asm volatile("" : "+v"(gd));
-          gd = cl >= cs ? gd : 0.0f;
-          a4[e] = cl > cs ? blv[e] * gd * kk[r] : 0.0f;
-          aqk_s[cl * CP + cs] = (bf16)(scale * gd * qk[r]);
+          gd = sc <= l ? gd : 0.0f;
+          at_s[sc * AS + l] = sc < l ? bel * gd * kk[r] : 0.0f;  // A^T[s][l]
+          q4[e] = (bf16)(scale * gd * qk[r]);
         }
-        *reinterpret_cast<float4*>(at_s + cs * AS + cl0) = make_float4(a4[0], a4[1], a4[2], a4[3]);
+        *reinterpret_cast<uint2*>(aqk_s + l * CP + s0) = *reinterpret_cast<uint2*>(q4);
       }
-    } else {
-      const int cs = 32 + col;
+    } else {  // the block l < 32 <= s of Aqk is zero
 #pragma unroll
-      for (int r = 0; r < 16; ++r) aqk_s[((r >> 2) * 8 + half * 4 + (r & 3)) * CP + cs] = (bf16)0.0f;
+      for (int g4 = 0; g4 < 4; ++g4)
+        *reinterpret_cast<uint2*>(aqk_s + col * CP + 32 + g4 * 8 + half * 4) = make_uint2(0u, 0u);
     }
     if (blk + gridDim.x < nblk) load(blk + gridDim.x, cur);  // operands consumed: next chunk
     lds_barrier();
