@@ -300,7 +300,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int gq = (m + 2) >> 2; gq < 4; ++gq) av[(m + 1) & 1][gq] = a4p[(m + 1) * (AS / 4) + gq];
         }
         const float t = (m == jl ? 1.0f : 0.0f) - p[m];
-        if (lane < 16) t_s[(base + m) * AS + base + jl] = t;
+        // every lane writes (the four 16-lane groups hold the same columns,
+        // so the writes agree): no exec-masked branch in the chain
+        t_s[(base + m) * AS + base + jl] = t;
 #pragma unroll
         for (int gq = (m + 1) >> 2; gq < 4; ++gq) {
           const float4 a4 = av[m & 1][gq];
