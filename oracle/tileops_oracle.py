@@ -2,8 +2,8 @@
 
 This module restates, in numpy (float32 opmath, float64 only where stated),
 the reference programs that define each operator's result in
-Yihuace/tile-ascendnpu-ops.  It is the checker the HIP kernels are compared
-with.  Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg
+Yihuace/tile-ascendnpu-ops; the HIP kernels' results are compared against
+it.  Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg
 may import it; the product path (tileops.*) never does.
 
 Storage types are modelled explicitly: a tensor is a float32 numpy array

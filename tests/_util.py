@@ -29,7 +29,7 @@ def ref_tolerance(dtype: torch.dtype) -> tuple[float, float]:
 
 
 # rtol = atol = 1e-2 for half-precision outputs at the benchmark configs
-NORTH_STAR_TOL = 1e-2
+HALF_PRECISION_TOL = 1e-2
 
 
 def assert_close_np(got: np.ndarray, ref: np.ndarray, atol: float, rtol: float, what: str = ""):
