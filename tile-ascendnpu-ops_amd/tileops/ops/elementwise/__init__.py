@@ -1,3 +1,4 @@
+from tileops.ops.elementwise.clamp_min import ClampMinFwdOp
 from tileops.ops.elementwise.clamp_scalar import ClampScalarFwdOp
 from tileops.ops.elementwise.gelu_and_mul import GeluAndMulFwdOp
 from tileops.ops.elementwise.gelu_tanh_and_mul import GeluTanhAndMulFwdOp
@@ -8,6 +9,7 @@ from tileops.ops.elementwise.isinf import IsinfFwdOp
 from tileops.ops.elementwise.isnan import IsnanFwdOp
 
 __all__ = [
+    "ClampMinFwdOp",
     "ClampScalarFwdOp",
     "GeluAndMulFwdOp",
     "GeluTanhAndMulFwdOp",
