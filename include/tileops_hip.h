@@ -144,13 +144,17 @@ int tileops_argreduce_fwd(const void* x, int64_t* y, int64_t M, int64_t N, int d
  *                               logsumexp(scale * q k^T, masked) / ln 2)
  * Causal masking is right-aligned: query i sees keys j <= i + (Skv - Sq).
  * H % Hkv == 0 (grouped-query sharing); D must be 64 or 128.
+ * softcap > 0 caps the scores, softcap * tanh(scale q.k / softcap), before
+ * the mask and the softmax (the lse is then of the capped scores); 0 turns
+ * it off; negative, NaN or infinite values are TILEOPS_EINVAL.
  * Replaces the npub::gqa_prefill_fwd_wrapped_kernel custom op called by
  * GQAPrefillFwdKernel.forward
  * (tileops/kernels/attention/multi_head_attention/multi_head_attention.py:77-124, 255-).
  */
 int tileops_mha_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                     int64_t B, int64_t Sq, int64_t Skv, int64_t H, int64_t Hkv,
-                    int64_t D, int causal, float scale, int dtype, void* stream);
+                    int64_t D, int causal, float scale, float softcap, int dtype,
+                    void* stream);
 
 /*
  * Chunked gated delta rule (gated DeltaNet) prefill, per (b, h):

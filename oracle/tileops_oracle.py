@@ -193,8 +193,12 @@ def argreduce(x: np.ndarray, axis: int = -1, is_min: bool = False) -> np.ndarray
 # ---------------------------------------------------------------------------
 # multi-head attention forward (BSHD)
 # ---------------------------------------------------------------------------
-def mha_fwd(q, k, v, is_causal: bool, dtype: str, scale: float | None = None):
+def mha_fwd(q, k, v, is_causal: bool, dtype: str, scale: float | None = None,
+            softcap: float = 0.0):
     """softmax(scale * q k^T [causal]) v per (b, h), plus the log2-domain LSE.
+    With softcap > 0 the scaled scores are capped first, softcap *
+    tanh(scores / softcap), then masked (golden_gqa_prefill_fwd,
+    perf_opt/_gqa_prefill_fwd_kernel.py:180-186).
 
     Output: F.scaled_dot_product_attention on BHSD transposes
     (tests/ops/test_multi_head_attention.py:32-45); LSE: logsumexp(scores) / ln 2
@@ -216,6 +220,8 @@ def mha_fwd(q, k, v, is_causal: bool, dtype: str, scale: float | None = None):
     for b in range(B):
         for h in range(H):
             s = (q[b, :, h, :] @ k[b, :, h // group, :].T) * scale
+            if softcap > 0.0:
+                s = softcap * np.tanh(s / softcap)
             if is_causal:
                 s = np.where(mask, -np.inf, s)
             m = s.max(axis=-1, keepdims=True)

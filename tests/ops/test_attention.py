@@ -24,7 +24,7 @@ CAUSAL_RTOL = 1e-2
 LSE_ATOL, LSE_RTOL = 1e-3, 1e-4
 
 
-def _check(q, k, v, o, lse, causal, pairs=None):
+def _check(q, k, v, o, lse, causal, pairs=None, softcap=0.0, rtol=None):
     qn, kn, vn = to_np(q), to_np(k), to_np(v)
     B, H = q.shape[0], q.shape[2]
     group = H // k.shape[2]
@@ -33,9 +33,11 @@ def _check(q, k, v, o, lse, causal, pairs=None):
     for b, h in pairs:
         hk = h // group
         o_ref, lse_ref = orc.mha_fwd(qn[b:b + 1, :, h:h + 1], kn[b:b + 1, :, hk:hk + 1],
-                                     vn[b:b + 1, :, hk:hk + 1], causal, NAMES[q.dtype])
-        assert_close_np(to_np(o[b:b + 1, :, h:h + 1]), o_ref, OUT_ATOL,
-                        CAUSAL_RTOL if causal else OUT_RTOL, f"o b{b} h{h}")
+                                     vn[b:b + 1, :, hk:hk + 1], causal, NAMES[q.dtype],
+                                     softcap=softcap)
+        if rtol is None:
+            rtol = CAUSAL_RTOL if causal else OUT_RTOL
+        assert_close_np(to_np(o[b:b + 1, :, h:h + 1]), o_ref, OUT_ATOL, rtol, f"o b{b} h{h}")
         assert_close_np(to_np(lse[b:b + 1, h:h + 1]), lse_ref, LSE_ATOL, LSE_RTOL,
                         f"lse b{b} h{h}")
 
@@ -98,6 +100,29 @@ def test_gqa_prefill_kernel(causal, sq, skv):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("softcap, dtype, D, sq, skv", [
+    (30.0, torch.bfloat16, 128, 256, 256),   # cap above every score: near the uncapped result
+    (2.0, torch.bfloat16, 128, 200, 333),    # tight cap: most scores saturate
+    (0.5, torch.float16, 64, 77, 77),        # ragged, tighter still
+    (5.0, torch.float16, 64, 64, 1024),
+])
+def test_gqa_prefill_softcap(causal, softcap, dtype, D, sq, skv):
+    # scores softcap * tanh(scale q.k / softcap) before the mask and the
+    # softmax (golden_gqa_prefill_fwd, perf_opt/_gqa_prefill_fwd_kernel.py:180-186).
+    # q is doubled so that rows are peaked and outputs reach |o| ~ 2-3, where one
+    # bf16 / fp16 ulp exceeds atol 5e-3: the half-precision rtol 1e-2 applies,
+    # as for causal rows.
+    B, H, Hkv = 2, 4, 2
+    q = torch.randn(B, sq, H, D, device="cuda", dtype=dtype) * 2
+    k = torch.randn(B, skv, Hkv, D, device="cuda", dtype=dtype)
+    v = torch.randn(B, skv, Hkv, D, device="cuda", dtype=dtype)
+    kern = GQAPrefillFwdKernel(B, H, Hkv, sq, skv, D, causal, dtype, softcap=softcap)
+    o, lse = kern(q, k, v)
+    _check(q, k, v, o, lse, causal, softcap=softcap, rtol=CAUSAL_RTOL)
+
+
+@pytest.mark.gpu
 def test_mha_peaked_attention():
     # one key per query dominates: exercises large score ranges and rescaling
     B, S, H, D = 1, 256, 2, 64
@@ -131,3 +156,7 @@ def test_gqa_kernel_contract():
         GQAPrefillFwdKernel(1, 6, 4, 64, 64, 64, False, torch.float16)
     with pytest.raises(ValueError, match="causal prefill"):
         GQAPrefillFwdKernel(1, 4, 4, 128, 64, 64, True, torch.float16)
+    for bad in (-1.0, float("nan"), float("inf")):
+        with pytest.raises(ValueError, match="softcap"):
+            GQAPrefillFwdKernel(1, 4, 4, 64, 64, 64, False, torch.float16, softcap=bad)
+    assert GQAPrefillFwdKernel(1, 4, 4, 64, 64, 64, False, torch.float16, softcap=30.0).softcap == 30.0

@@ -67,6 +67,12 @@ def test_host_side_argument_rejection(lib):
     # causal attention with more queries than keys (the right-aligned mask
     # would leave whole query blocks without a key) is rejected, as the Op does
     assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 333, 200, 2, 2, 128, 1, 1.0,
-                               2, None) == -2
+                               0.0, 2, None) == -2
     assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 333, 200, 2, 2, 128, 0, 1.0,
-                               2, None) == -3  # non-causal: fine until the null pointers
+                               0.0, 2, None) == -3  # non-causal: fine until the null pointers
+    # softcap: 0 is off, positive caps; negative, NaN and infinite are rejected
+    assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 64, 64, 2, 2, 128, 0, 1.0,
+                               30.0, 2, None) == -3
+    for bad in (-1.0, float("nan"), float("inf")):
+        assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 64, 64, 2, 2, 128, 0, 1.0,
+                                   bad, 2, None) == -1, bad

@@ -238,6 +238,36 @@ def test_mha_uniform_attention_closed_form():
     np.testing.assert_allclose(o[0, :, 0], np.broadcast_to(v[0, :, 0].mean(0), (S, D)), rtol=1e-6)
 
 
+def test_mha_softcap_limits_and_closed_forms():
+    """Soft-capping (scores -> c tanh(scores / c), applied to the scaled scores
+    before the mask, as golden_gqa_prefill_fwd does): a huge cap is the
+    uncapped attention; one key gives lse = capped score / ln 2; two keys
+    with scaled scores 2 and 0 under c = 1 weigh sigmoid(tanh 2) : 1 - that;
+    a tiny cap flattens every row to uniform attention."""
+    rng = np.random.default_rng(9)
+    B, S, H, D = 1, 24, 2, 8
+    q, k, v = (rng.standard_normal((B, S, H, D)).astype(np.float32) for _ in range(3))
+    for causal in (False, True):
+        o0, l0 = orc.mha_fwd(q, k, v, causal, "float32")
+        o1, l1 = orc.mha_fwd(q, k, v, causal, "float32", softcap=1e6)
+        np.testing.assert_allclose(o1, o0, rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(l1, l0, rtol=1e-5, atol=1e-6)
+    # scale * q.k = 0.5 * 4 = 2 for the first key, 0 for the second
+    q1 = np.ones((1, 1, 1, 4), np.float32)
+    k2 = np.stack([np.ones(4), np.zeros(4)]).astype(np.float32).reshape(1, 2, 1, 4)
+    v2 = np.array([[1.0, 0, 0, 0], [0, 1.0, 0, 0]], np.float32).reshape(1, 2, 1, 4)
+    o, lse = orc.mha_fwd(q1, k2[:, :1], v2[:, :1], False, "float32", scale=0.5, softcap=1.0)
+    assert abs(lse[0, 0, 0] - 0.9640275800758169 / math.log(2.0)) < 1e-6  # tanh(2)
+    np.testing.assert_allclose(o[0, 0, 0], v2[0, 0, 0], rtol=1e-6)
+    o, lse = orc.mha_fwd(q1, k2, v2, False, "float32", scale=0.5, softcap=1.0)
+    w1 = 1.0 / (1.0 + math.exp(-0.9640275800758169))
+    np.testing.assert_allclose(o[0, 0, 0], [w1, 1.0 - w1, 0.0, 0.0], rtol=1e-6, atol=1e-7)
+    # tiny cap: every capped score within 1e-3 of 0 -> near-uniform rows
+    o, lse = orc.mha_fwd(q, k, v, False, "float32", softcap=1e-3)
+    np.testing.assert_allclose(o[0, :, 0], np.broadcast_to(v[0, :, 0].mean(0), (S, D)), atol=1e-3)
+    np.testing.assert_allclose(lse, math.log2(S), atol=1e-2)
+
+
 # -- gated delta rule -----------------------------------------------------------------
 def _gdn_inputs(B=2, T=37, H=2, K=8, V=6, seed=7, h0=True):
     rng = np.random.default_rng(seed)

@@ -144,10 +144,22 @@ __device__ __forceinline__ void gather_offsets(uint32_t (&off)[BN * D / 2048], i
 // (each group ends its softmax phase waiting for everything but the windows
 // it just issued: vmcnt(4) for D = 128, vmcnt(2) for D = 64, vmcnt(0) when
 // it issued none).
-template <typename T, int D, bool CAUSAL, int BN>
+// tanh(y) = 1 - 2 / (1 + e^{2y}), saturating to +-1 through the
+// exponential's overflow / underflow (no branch)
+__device__ __forceinline__ float tanh_sat(float y) {
+  const float e = __builtin_amdgcn_exp2f(y * (2.0f * 1.4426950408889634f));
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// SOFTCAP: scores are capped, softcap * tanh(scale q.k / softcap) (the
+// reference's order: scale, cap, then the causal mask), and carried in log2
+// units from the start of the softmax: the caller passes scale_log2 = 1,
+// cap_scale = scale / softcap and cap_log2 = softcap * log2 e.
+template <typename T, int D, bool CAUSAL, int BN, bool SOFTCAP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void mha_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
-    float* __restrict__ lse, int B, int Sq, int Skv, int H, int Hkv, float scale_log2, int nqb) {
+    float* __restrict__ lse, int B, int Sq, int Skv, int H, int Hkv, float scale_log2, int nqb,
+    float cap_scale, float cap_log2) {
   typedef typename Mfma<T>::V8 V8;
   constexpr int NKB = BN / 32;    // 32-key blocks per tile
   constexpr int BM = 256;         // query rows per workgroup (8 x 32)
@@ -250,7 +262,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int i = 0; i < DBLK; ++i) acc_o[i] = f32x16{};
   f32x16 acc_s[NKB];
   V8 pb[2 * NKB];
-  float m_run = -INFINITY;  // running max of raw scores (q . k)
+  float m_run = -INFINITY;  // running max of raw scores q . k (capped, log2 units with SOFTCAP)
   float l_run = 0.0f;
   const float lazy_raw = kLazyLog2 / scale_log2;
 
@@ -356,6 +368,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // online softmax of tile t for query row qi: maxima in raw score units,
   // the scale (times log2 e) folded into one FMA per score inside exp2
   auto softmax = [&](int t) __device__ __attribute__((always_inline)) {
+    if constexpr (SOFTCAP) {  // capped scores in log2 units (monotone: the row max is kept)
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_s[kb][r] = cap_log2 * tanh_sat(acc_s[kb][r] * cap_scale);
+      }
+    }
     const int kv0 = t * BN;
     // masking only on the ragged last tile and on causal diagonal tiles
     // (a workgroup-uniform branch, kept out of the common path)
@@ -494,37 +513,46 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
-template <typename T, int D, int BN>
-static int launch(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Sq,
-                  int Skv, int H, int Hkv, bool causal, float scale, hipStream_t s) {
+template <typename T, int D, int BN, bool SOFTCAP>
+static void launch_k(const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                     int Sq, int Skv, int H, int Hkv, bool causal, float sl2, float cap_scale,
+                     float cap_log2, hipStream_t s) {
   constexpr int BM = 256;
   const int nqb = (Sq + BM - 1) / BM;
   const int64_t total = (int64_t)nqb * H * B;
-  const float scale_log2 = scale * 1.4426950408889634f;
   dim3 grid((unsigned)total), block(512);
   if (causal)
-    mha_fwd_kernel<T, D, true, BN><<<grid, block, 0, s>>>(
+    mha_fwd_kernel<T, D, true, BN, SOFTCAP><<<grid, block, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-        static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, scale_log2, nqb);
+        static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, sl2, nqb, cap_scale, cap_log2);
   else
-    mha_fwd_kernel<T, D, false, BN><<<grid, block, 0, s>>>(
+    mha_fwd_kernel<T, D, false, BN, SOFTCAP><<<grid, block, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-        static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, scale_log2, nqb);
-  return launch_status();
+        static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, sl2, nqb, cap_scale, cap_log2);
 }
 
 template <typename T, int D>
 static int launch_w(const void* q, const void* k, const void* v, void* o, float* lse, int B,
-                    int Sq, int Skv, int H, int Hkv, bool causal, float scale, hipStream_t s) {
-  return launch<T, D, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
+                    int Sq, int Skv, int H, int Hkv, bool causal, float scale, float softcap,
+                    hipStream_t s) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  if (softcap > 0.0f)
+    launch_k<T, D, 64, true>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, 1.0f, scale / softcap,
+                             softcap * kLog2e, s);
+  else
+    launch_k<T, D, 64, false>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale * kLog2e, 0.0f,
+                              0.0f, s);
+  return launch_status();
 }
 
 template <typename T>
 static int dispatch_d(int D, const void* q, const void* k, const void* v, void* o, float* lse,
                       int B, int Sq, int Skv, int H, int Hkv, bool causal, float scale,
-                      hipStream_t s) {
-  if (D == 128) return launch_w<T, 128>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
-  if (D == 64) return launch_w<T, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, s);
+                      float softcap, hipStream_t s) {
+  if (D == 128)
+    return launch_w<T, 128>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
+  if (D == 64)
+    return launch_w<T, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
   return TILEOPS_ESHAPE;
 }
 
@@ -535,12 +563,14 @@ using namespace tileops;
 
 extern "C" int tileops_mha_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                                int64_t B, int64_t Sq, int64_t Skv, int64_t H, int64_t Hkv,
-                               int64_t D, int causal, float scale, int dtype, void* stream) {
+                               int64_t D, int causal, float scale, float softcap, int dtype,
+                               void* stream) {
   if (B < 0 || Sq < 0 || Skv < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0) return TILEOPS_ESHAPE;
   if (D != 64 && D != 128) return TILEOPS_ESHAPE;
   if (B > INT32_MAX || Sq > INT32_MAX || Skv > INT32_MAX || H > 65535) return TILEOPS_ESHAPE;
   if (causal && Sq > Skv) return TILEOPS_ESHAPE;
   if (dtype != TILEOPS_F16 && dtype != TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (!(softcap >= 0.0f) || !(softcap < INFINITY)) return TILEOPS_EINVAL;  // NaN, < 0, inf
   if (B == 0 || Sq == 0) return 0;
   if (Skv == 0) return TILEOPS_ESHAPE;
   if (!q || !k || !v || !o || !lse) return TILEOPS_ENULL;
@@ -550,7 +580,7 @@ extern "C" int tileops_mha_fwd(const void* q, const void* k, const void* v, void
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TILEOPS_BF16)
     return mha::dispatch_d<bf16>((int)D, q, k, v, o, lse, (int)B, (int)Sq, (int)Skv, (int)H,
-                                 (int)Hkv, causal != 0, scale, s);
+                                 (int)Hkv, causal != 0, scale, softcap, s);
   return mha::dispatch_d<f16>((int)D, q, k, v, o, lse, (int)B, (int)Sq, (int)Skv, (int)H,
-                              (int)Hkv, causal != 0, scale, s);
+                              (int)Hkv, causal != 0, scale, softcap, s);
 }

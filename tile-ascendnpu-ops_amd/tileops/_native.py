@@ -62,7 +62,7 @@ SIGNATURES = {
         [
             _c_p, _c_p, _c_p, _c_p, _c_p,
             _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-            _c_int, _c_float, _c_int, _c_p,
+            _c_int, _c_float, _c_float, _c_int, _c_p,
         ],
     ),
     "tileops_gdn_prefill_fwd": (

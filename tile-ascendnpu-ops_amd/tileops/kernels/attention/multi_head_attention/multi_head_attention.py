@@ -31,6 +31,7 @@ def _gqa_prefill_fwd(
     dim: int,
     is_causal: bool,
     sm_scale: float,
+    softcap: float,
     q: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
@@ -40,7 +41,7 @@ def _gqa_prefill_fwd(
     code = _native.lib().tileops_mha_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
         batch, seq_len_q, seq_len_kv, heads, heads_kv, dim,
-        1 if is_causal else 0, float(sm_scale), _native.dtype_code(q.dtype),
+        1 if is_causal else 0, float(sm_scale), float(softcap), _native.dtype_code(q.dtype),
         _native.stream_of(q),
     )
     _native.check(code, "tileops_mha_fwd")
@@ -48,7 +49,7 @@ def _gqa_prefill_fwd(
 
 
 @_gqa_prefill_fwd.register_fake
-def _(batch, heads, heads_kv, seq_len_q, seq_len_kv, dim, is_causal, sm_scale, q, k, v):
+def _(batch, heads, heads_kv, seq_len_q, seq_len_kv, dim, is_causal, sm_scale, softcap, q, k, v):
     return torch.empty_like(q), q.new_empty((batch, heads, seq_len_q), dtype=torch.float32)
 
 
@@ -61,7 +62,8 @@ class GQAPrefillFwdKernel(Kernel):
         is_causal: Apply the right-aligned causal mask.
         dtype: float16 or bfloat16.
         sm_scale: Softmax scale (default ``dim ** -0.5``).
-        softcap: Score soft-capping; only ``0.0`` (off) is implemented.
+        softcap: Score soft-capping, ``softcap * tanh(scale q.k / softcap)`` before the
+            mask and the softmax; ``0.0`` (default) turns it off.
         config: Optional config override.
     """
 
@@ -95,8 +97,8 @@ class GQAPrefillFwdKernel(Kernel):
             )
         if dim not in (64, 128):
             raise ValueError(f"{self.__class__.__name__} supports dim 64 or 128, got {dim}")
-        if softcap != 0.0:
-            raise ValueError(f"{self.__class__.__name__}: softcap is not supported (got {softcap})")
+        if not (0.0 <= softcap < float("inf")):
+            raise ValueError(f"{self.__class__.__name__}: softcap must be finite and >= 0 (got {softcap})")
         self.batch = batch
         self.heads = heads
         self.heads_kv = heads_kv
@@ -130,5 +132,6 @@ class GQAPrefillFwdKernel(Kernel):
                 raise ValueError(f"Expected {name}.dtype {self.dtype}, got {t.dtype}")
         return _gqa_prefill_fwd(
             self.batch, self.heads, self.heads_kv, self.seq_len_q, self.seq_len_kv, self.dim,
-            self.is_causal, self.sm_scale, q.contiguous(), k.contiguous(), v.contiguous(),
+            self.is_causal, self.sm_scale, self.softcap, q.contiguous(), k.contiguous(),
+            v.contiguous(),
         )
