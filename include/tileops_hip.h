@@ -179,6 +179,23 @@ int tileops_gdn_prefill_fwd(const void* q, const void* k, const void* v,
 size_t tileops_gdn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K,
                                            int64_t V, int64_t chunk);
 
+/*
+ * Single-token gated linear attention decode, layout BHD, per (b, h):
+ *   new_state[dk][dv] = exp(gk[dk]) * state[dk][dv] + k[dk] * v[dv]
+ *   o[dv]             = scale * sum_dk q[dk] * new_state[dk][dv]
+ * q, k, gk: [B, H, DK]   v, o: [B, H, DV]   state, new_state: [B, H, DK, DV],
+ * all of `dtype` (F32, F16 or BF16); fp32 arithmetic, the readout from the
+ * unrounded new state.  scale > 0 (the caller resolves its default
+ * DK ** -0.5).  DV <= 256, or DV * element size a multiple of 16 with at
+ * most 256 such 16-byte groups (TILEOPS_ESHAPE otherwise).
+ * Replaces the kernel program GLADecodeKernel.forward runs
+ * (tileops/kernels/linear_attention/gla_decode/gla_decode.py:57-66; op
+ * interface tileops/ops/linear_attention/gla_decode.py:24-77).
+ */
+int tileops_gla_decode_fwd(const void* q, const void* k, const void* v, const void* gk,
+                           const void* state, void* o, void* new_state, int64_t B, int64_t H,
+                           int64_t DK, int64_t DV, float scale, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

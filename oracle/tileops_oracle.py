@@ -233,6 +233,25 @@ def mha_fwd(q, k, v, is_causal: bool, dtype: str, scale: float | None = None,
 
 
 # ---------------------------------------------------------------------------
+# gated linear attention (GLA) decode
+# ---------------------------------------------------------------------------
+def gla_decode(q, k, v, gk, state, scale: float, dtype: str):
+    """One GLA decode step, restating golden_gla_decode
+    (tileops/kernels/linear_attention/gla_decode/gla_decode_kernel/
+    _gla_decode_kernel.py:211-218), layout BHD:
+
+        new_state = exp(gk)[..., None] * state + k[..., None] * v[..., None, :]
+        o         = scale * einsum("bhk,bhkv->bhv", q, new_state)
+
+    fp64 arithmetic, the readout from the unrounded new state; both outputs
+    rounded once to ``dtype``."""
+    q, k, v, gk, s = (np.asarray(a, np.float64) for a in (q, k, v, gk, state))
+    ns = np.exp(gk)[..., None] * s + k[..., :, None] * v[..., None, :]
+    o = scale * np.einsum("bhk,bhkv->bhv", q, ns)
+    return round_to(dtype, o.astype(np.float32)), round_to(dtype, ns.astype(np.float32))
+
+
+# ---------------------------------------------------------------------------
 # gated delta rule (GDN) prefill
 # ---------------------------------------------------------------------------
 def gdn_sequential(q, k, v, g, beta, h0, scale: float):

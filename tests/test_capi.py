@@ -30,7 +30,8 @@ def test_header_declares_the_expected_entry_points():
     names = _declared_functions()
     for required in ("tileops_unary_fwd", "tileops_isfp_fwd", "tileops_gated_gelu_fwd",
                      "tileops_fused_add_layernorm_fwd", "tileops_logsumexp_fwd",
-                     "tileops_argreduce_fwd", "tileops_mha_fwd", "tileops_gdn_prefill_fwd"):
+                     "tileops_argreduce_fwd", "tileops_mha_fwd", "tileops_gdn_prefill_fwd",
+                     "tileops_gla_decode_fwd"):
         assert required in names
 
 
@@ -70,6 +71,13 @@ def test_host_side_argument_rejection(lib):
                                0.0, 2, None) == -2
     assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 333, 200, 2, 2, 128, 0, 1.0,
                                0.0, 2, None) == -3  # non-causal: fine until the null pointers
+    # GLA decode: positive sizes and scale, then the null pointers
+    assert lib.tileops_gla_decode_fwd(None, None, None, None, None, None, None, 1, 2, 0, 64,
+                                      0.1, 1, None) == -2
+    assert lib.tileops_gla_decode_fwd(None, None, None, None, None, None, None, 1, 2, 64, 64,
+                                      -1.0, 1, None) == -1
+    assert lib.tileops_gla_decode_fwd(None, None, None, None, None, None, None, 1, 2, 64, 64,
+                                      0.1, 1, None) == -3
     # softcap: 0 is off, positive caps; negative, NaN and infinite are rejected
     assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 64, 64, 2, 2, 128, 0, 1.0,
                                30.0, 2, None) == -3

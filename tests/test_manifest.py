@@ -26,7 +26,7 @@ HOT_PATH_OPS = {
     "LogSumExpFwdOp", "ArgmaxFwdOp", "MultiHeadAttentionFwdOp", "GatedDeltaNetPrefillFwdOp",
 }
 # ops beyond the hot path built on its kernels (the clamp kernel without an upper bound)
-WIDENED_OPS = {"ClampMinFwdOp"}
+WIDENED_OPS = {"ClampMinFwdOp", "GLADecodeOp"}
 
 
 def test_manifest_holds_the_hot_path_ops():
@@ -147,6 +147,7 @@ def _static_ops():
     from tileops.ops.elementwise.isinf import IsinfFwdOp
     from tileops.ops.elementwise.isnan import IsnanFwdOp
     from tileops.ops.linear_attention.gdn_prefill import GatedDeltaNetPrefillFwdOp
+    from tileops.ops.linear_attention.gla_decode import GLADecodeOp
 
     def flat(cls):
         def make(w, dt):
@@ -173,6 +174,8 @@ def _static_ops():
         "MultiHeadAttentionFwdOp": lambda w, dt: MultiHeadAttentionFwdOp(
             w["q_shape"][0], w["q_shape"][2], w["q_shape"][1], w["q_shape"][3],
             w.get("is_causal", True), dt),
+        "GLADecodeOp": lambda w, dt: GLADecodeOp(w["B"], w["H"], w["DK"], w["DV"],
+                                                 scale=w.get("scale", -1.0), dtype=dt),
         "GatedDeltaNetPrefillFwdOp": lambda w, dt: GatedDeltaNetPrefillFwdOp(
             w["batch"], w["seq_len"], w["heads"], w["dim_k"], w["dim_v"], dtype=dt),
     }

@@ -268,6 +268,29 @@ def test_mha_softcap_limits_and_closed_forms():
     np.testing.assert_allclose(lse, math.log2(S), atol=1e-2)
 
 
+# -- GLA decode -------------------------------------------------------------------------
+def test_gla_decode_closed_forms():
+    """gk = 0 and a zero state leave new_state = k v^T and o = scale (q.k) v;
+    k = 0 leaves a pure decay, new_state = e^gk state, read out as
+    scale q^T (e^gk state); the two add up (the update is linear in the state
+    and in k v^T)."""
+    rng = np.random.default_rng(12)
+    B, H, DK, DV, scale = 2, 3, 8, 5, 0.3
+    q, k, gk = (rng.standard_normal((B, H, DK)) for _ in range(3))
+    v = rng.standard_normal((B, H, DV))
+    s0 = rng.standard_normal((B, H, DK, DV))
+    o, ns = orc.gla_decode(q, k, v, np.zeros_like(gk), np.zeros_like(s0), scale, "float32")
+    np.testing.assert_allclose(ns, np.einsum("bhk,bhv->bhkv", k, v), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(o, scale * (q * k).sum(-1)[..., None] * v, rtol=1e-5, atol=1e-6)
+    o2, ns2 = orc.gla_decode(q, np.zeros_like(k), v, gk, s0, scale, "float32")
+    decayed = np.exp(gk)[..., None] * s0
+    np.testing.assert_allclose(ns2, decayed, rtol=1e-6, atol=1e-6)
+    want = scale * np.stack([[q[b, h] @ decayed[b, h] for h in range(H)] for b in range(B)])
+    np.testing.assert_allclose(o2, want, rtol=1e-5, atol=1e-6)
+    o3, ns3 = orc.gla_decode(q, k, v, gk, s0, scale, "float32")
+    np.testing.assert_allclose(ns3, ns2 + np.einsum("bhk,bhv->bhkv", k, v), rtol=1e-5, atol=1e-6)
+
+
 # -- gated delta rule -----------------------------------------------------------------
 def _gdn_inputs(B=2, T=37, H=2, K=8, V=6, seed=7, h0=True):
     rng = np.random.default_rng(seed)

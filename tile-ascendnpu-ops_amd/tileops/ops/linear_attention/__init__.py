@@ -1,3 +1,4 @@
 from tileops.ops.linear_attention.gdn_prefill import GatedDeltaNetPrefillFwdOp
+from tileops.ops.linear_attention.gla_decode import GLADecodeOp
 
-__all__ = ["GatedDeltaNetPrefillFwdOp"]
+__all__ = ["GLADecodeOp", "GatedDeltaNetPrefillFwdOp"]
