@@ -37,6 +37,7 @@ enum tileops_unary_op {
   TILEOPS_HARDSWISH = 0,
   TILEOPS_HARDSIGMOID = 1,
   TILEOPS_CLAMP = 2,
+  TILEOPS_MISH = 3,
 };
 
 /* Float predicate selector for tileops_isfp_fwd. */
@@ -69,13 +70,15 @@ const char* tileops_error_string(int code);
  *   TILEOPS_CLAMP       min(max(x, lo), hi) with the bounds selected by
  *                       `flags` (TILEOPS_CLAMP_HAS_MIN / _HAS_MAX, at least
  *                       one); a NaN bound yields NaN everywhere.
+ *   TILEOPS_MISH        x * tanh(log1p(exp(x)))  (F.mish)
  * NaN inputs propagate.  x and y may alias (in-place).
  * Replaces HardswishFwdKernel.forward
  * (tileops/kernels/elementwise/hardswish/hardswish.py:145-156),
  * HardsigmoidFwdKernel.forward
  * (tileops/kernels/elementwise/hardsigmoid/hardsigmoid.py:147) and
  * ClampScalarFwdKernel.forward
- * (tileops/kernels/elementwise/clamp_scalar/clamp_scalar.py:174-190).
+ * (tileops/kernels/elementwise/clamp_scalar/clamp_scalar.py:174-190) and
+ * MishFwdKernel.forward (tileops/kernels/elementwise/mish/mish.py).
  */
 int tileops_unary_fwd(int op, const void* x, void* y, int64_t n, int dtype,
                       float lo, float hi, int flags, void* stream);

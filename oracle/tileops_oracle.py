@@ -81,6 +81,15 @@ def hardsigmoid(x: np.ndarray, dtype: str) -> np.ndarray:
     return round_to(dtype, t / np.float32(6))
 
 
+def mish(x: np.ndarray, dtype: str) -> np.ndarray:
+    """F.mish(x.float()).to(dtype) -- tests/ops/test_mish.py:38-39:
+    x * tanh(log1p(exp(x))), fp64 arithmetic, rounded once."""
+    xd = np.asarray(x, np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = xd * np.tanh(np.log1p(np.exp(xd)))
+    return round_to(dtype, y.astype(np.float32))
+
+
 def clamp_scalar(x: np.ndarray, dtype: str, lo=None, hi=None) -> np.ndarray:
     """torch.clamp(x.float(), min, max).to(dtype) -- tests/ops/test_clamp_scalar.py:56-57.
     NaN inputs propagate, a NaN bound gives NaN, min > max gives max."""

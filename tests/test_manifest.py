@@ -26,7 +26,7 @@ HOT_PATH_OPS = {
     "LogSumExpFwdOp", "ArgmaxFwdOp", "MultiHeadAttentionFwdOp", "GatedDeltaNetPrefillFwdOp",
 }
 # ops beyond the hot path built on its kernels (the clamp kernel without an upper bound)
-WIDENED_OPS = {"ClampMinFwdOp", "GLADecodeOp"}
+WIDENED_OPS = {"ClampMinFwdOp", "GLADecodeOp", "MishFwdOp"}
 
 
 def test_manifest_holds_the_hot_path_ops():
@@ -146,6 +146,7 @@ def _static_ops():
     from tileops.ops.elementwise.isfinite import IsfiniteFwdOp
     from tileops.ops.elementwise.isinf import IsinfFwdOp
     from tileops.ops.elementwise.isnan import IsnanFwdOp
+    from tileops.ops.elementwise.mish import MishFwdOp
     from tileops.ops.linear_attention.gdn_prefill import GatedDeltaNetPrefillFwdOp
     from tileops.ops.linear_attention.gla_decode import GLADecodeOp
 
@@ -167,6 +168,7 @@ def _static_ops():
         "ClampScalarFwdOp": flat(ClampScalarFwdOp),
         "ClampMinFwdOp": flat(ClampMinFwdOp),
         "IsnanFwdOp": flat(IsnanFwdOp),
+        "MishFwdOp": flat(MishFwdOp),
         "IsinfFwdOp": flat(IsinfFwdOp),
         "IsfiniteFwdOp": flat(IsfiniteFwdOp),
         "GeluAndMulFwdOp": gated(GeluAndMulFwdOp),

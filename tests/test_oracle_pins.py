@@ -207,6 +207,20 @@ def test_argmax_other_axis_and_flat():
     assert orc.argreduce(x.reshape(1, -1), -1)[0] == torch.from_numpy(x).argmax().item()
 
 
+def test_mish_matches_torch():
+    x = np.concatenate([np.linspace(-30, 30, 4001), [0.0, -0.0, 60.0, -60.0, 100.0, -100.0,
+                                                      np.inf, -np.inf, np.nan]]).astype(np.float32)
+    for dt, tdt in (("float32", torch.float32), ("float16", torch.float16),
+                    ("bfloat16", torch.bfloat16)):
+        xd = orc.round_to(dt, x)
+        want = torch.nn.functional.mish(torch.from_numpy(xd)).to(tdt).float().numpy()
+        got = orc.mish(xd, dt)
+        assert np.array_equal(np.isnan(got), np.isnan(want)), dt
+        ok = ~np.isnan(want)
+        atol = {"float32": 1e-6, "float16": 1e-3, "bfloat16": 1e-2}[dt]
+        np.testing.assert_allclose(got[ok], want[ok], rtol=atol, atol=atol, err_msg=dt)
+
+
 # -- attention -----------------------------------------------------------------------
 @pytest.mark.parametrize("causal", [False, True])
 def test_mha_matches_sdpa(causal):

@@ -44,6 +44,16 @@ __device__ __forceinline__ float unary_op(float x, float lo, float hi, int flags
     t = t < 0.0f ? 0.0f : t;
     t = t > 6.0f ? 6.0f : t;
     return div6(t);
+  } else if constexpr (OP == TILEOPS_MISH) {
+    // x * tanh(softplus(x)) (F.mish, test_mish.py:38-39) through
+    // tanh(log(1 + u)) = n / (n + 2) with n = u (u + 2), u = e^x: one
+    // exponential and one reciprocal instead of exp, log1p and tanh.  Above
+    // x = 20 the factor is 1 in fp32 (and n would overflow), so x itself.
+    // +inf -> +inf, -inf -> NaN (-inf * 0), NaN -> NaN, as F.mish gives.
+    const float u = __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+    const float n = u * (u + 2.0f);
+    const float t = n * __builtin_amdgcn_rcpf(n + 2.0f);
+    return x * (x > 20.0f ? 1.0f : t);
   } else {
     // torch.clamp(x, min, max) (test_clamp_scalar.py:56-57): NaN input stays
     // NaN; a NaN bound selects the bound itself, i.e. NaN everywhere; with
@@ -114,6 +124,7 @@ static int dispatch_unary(int op, const void* x, void* y, int64_t n, float lo, f
     case TILEOPS_HARDSIGMOID:
       return launch_unary<T, TILEOPS_HARDSIGMOID>(x, y, n, lo, hi, flags, s);
     case TILEOPS_CLAMP: return launch_unary<T, TILEOPS_CLAMP>(x, y, n, lo, hi, flags, s);
+    case TILEOPS_MISH: return launch_unary<T, TILEOPS_MISH>(x, y, n, lo, hi, flags, s);
   }
   return TILEOPS_EINVAL;
 }
@@ -363,7 +374,7 @@ extern "C" int tileops_unary_fwd(int op, const void* x, void* y, int64_t n, int 
   if (n < 0) return TILEOPS_ESHAPE;
   if (op == TILEOPS_CLAMP && (flags & (TILEOPS_CLAMP_HAS_MIN | TILEOPS_CLAMP_HAS_MAX)) == 0)
     return TILEOPS_EINVAL;
-  if (op < TILEOPS_HARDSWISH || op > TILEOPS_CLAMP) return TILEOPS_EINVAL;
+  if (op < TILEOPS_HARDSWISH || op > TILEOPS_MISH) return TILEOPS_EINVAL;
   if (dtype < TILEOPS_F32 || dtype > TILEOPS_BF16) return TILEOPS_EINVAL;
   if (n == 0) return 0;
   if (!x || !y) return TILEOPS_ENULL;

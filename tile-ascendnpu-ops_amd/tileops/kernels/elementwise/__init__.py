@@ -6,6 +6,7 @@ from tileops.kernels.elementwise.hardswish import HardswishFwdKernel
 from tileops.kernels.elementwise.isfinite import IsfiniteFwdKernel
 from tileops.kernels.elementwise.isinf import IsinfFwdKernel
 from tileops.kernels.elementwise.isnan import IsnanFwdKernel
+from tileops.kernels.elementwise.mish import MishFwdKernel
 
 __all__ = [
     "ClampScalarFwdKernel",
@@ -16,4 +17,5 @@ __all__ = [
     "IsfiniteFwdKernel",
     "IsinfFwdKernel",
     "IsnanFwdKernel",
+    "MishFwdKernel",
 ]

@@ -20,7 +20,7 @@ from tileops.kernels.kernel_base import Kernel
 _FLOAT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 # enum tileops_unary_op / tileops_predicate (include/tileops_hip.h)
-HARDSWISH, HARDSIGMOID, CLAMP = 0, 1, 2
+HARDSWISH, HARDSIGMOID, CLAMP, MISH = 0, 1, 2, 3
 ISNAN, ISINF, ISFINITE = 0, 1, 2
 CLAMP_HAS_MIN, CLAMP_HAS_MAX = 1, 2
 

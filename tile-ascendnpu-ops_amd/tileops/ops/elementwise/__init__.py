@@ -7,6 +7,7 @@ from tileops.ops.elementwise.hardswish import HardswishFwdOp
 from tileops.ops.elementwise.isfinite import IsfiniteFwdOp
 from tileops.ops.elementwise.isinf import IsinfFwdOp
 from tileops.ops.elementwise.isnan import IsnanFwdOp
+from tileops.ops.elementwise.mish import MishFwdOp
 
 __all__ = [
     "ClampMinFwdOp",
@@ -18,4 +19,5 @@ __all__ = [
     "IsfiniteFwdOp",
     "IsinfFwdOp",
     "IsnanFwdOp",
+    "MishFwdOp",
 ]

@@ -32,6 +32,10 @@ class HardswishWorkload(ShapedRandnWorkload):
     """Input of HardswishFwdOp."""
 
 
+class MishWorkload(ShapedRandnWorkload):
+    """Input of MishFwdOp: randn of the workload shape."""
+
+
 class ClampScalarWorkload(ShapedRandnWorkload):
     """Input of ClampScalarFwdOp (the bounds are op parameters)."""
 
