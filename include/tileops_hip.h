@@ -84,6 +84,16 @@ int tileops_unary_fwd(int op, const void* x, void* y, int64_t n, int dtype,
                       float lo, float hi, int flags, void* stream);
 
 /*
+ * y = torch.bitwise_not(x) over `nbytes` bytes of a bool or integer tensor
+ * (uint8 / int8 / int16 / int32 / int64): every byte complemented, or, for
+ * bool (is_bool != 0, bytes 0 / 1), every byte XOR 1.  x and y may alias.
+ * Replaces BitwiseNotFwdKernel.forward
+ * (tileops/kernels/elementwise/bitwise_not/bitwise_not.py; op interface
+ * tileops/ops/elementwise/bitwise_not.py:33-120).
+ */
+int tileops_bitwise_not_fwd(const void* x, void* y, int64_t nbytes, int is_bool, void* stream);
+
+/*
  * y[i] = pred(x[i]) as one byte 0/1 (torch.bool storage), i < n.
  * Replaces IsnanFwdKernel.forward (tileops/kernels/elementwise/isnan/isnan.py:142-156),
  * IsinfFwdKernel.forward (tileops/kernels/elementwise/isinf/isinf.py:150) and

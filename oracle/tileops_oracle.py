@@ -81,6 +81,13 @@ def hardsigmoid(x: np.ndarray, dtype: str) -> np.ndarray:
     return round_to(dtype, t / np.float32(6))
 
 
+def bitwise_not(x: np.ndarray) -> np.ndarray:
+    """torch.bitwise_not(x) (tests/ops/test_bitwise_not.py of the reference):
+    the complement of every integer, logical NOT of a bool."""
+    x = np.asarray(x)
+    return np.logical_not(x) if x.dtype == np.bool_ else np.invert(x)
+
+
 def mish(x: np.ndarray, dtype: str) -> np.ndarray:
     """F.mish(x.float()).to(dtype) -- tests/ops/test_mish.py:38-39:
     x * tanh(log1p(exp(x))), fp64 arithmetic, rounded once."""

@@ -31,7 +31,7 @@ def test_header_declares_the_expected_entry_points():
     for required in ("tileops_unary_fwd", "tileops_isfp_fwd", "tileops_gated_gelu_fwd",
                      "tileops_fused_add_layernorm_fwd", "tileops_logsumexp_fwd",
                      "tileops_argreduce_fwd", "tileops_mha_fwd", "tileops_gdn_prefill_fwd",
-                     "tileops_gla_decode_fwd"):
+                     "tileops_gla_decode_fwd", "tileops_bitwise_not_fwd"):
         assert required in names
 
 
@@ -71,6 +71,9 @@ def test_host_side_argument_rejection(lib):
                                0.0, 2, None) == -2
     assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 333, 200, 2, 2, 128, 0, 1.0,
                                0.0, 2, None) == -3  # non-causal: fine until the null pointers
+    assert lib.tileops_bitwise_not_fwd(None, None, -1, 0, None) == -2
+    assert lib.tileops_bitwise_not_fwd(None, None, 0, 0, None) == 0
+    assert lib.tileops_bitwise_not_fwd(None, None, 16, 1, None) == -3
     # GLA decode: positive sizes and scale, then the null pointers
     assert lib.tileops_gla_decode_fwd(None, None, None, None, None, None, None, 1, 2, 0, 64,
                                       0.1, 1, None) == -2

@@ -26,7 +26,7 @@ HOT_PATH_OPS = {
     "LogSumExpFwdOp", "ArgmaxFwdOp", "MultiHeadAttentionFwdOp", "GatedDeltaNetPrefillFwdOp",
 }
 # ops beyond the hot path built on its kernels (the clamp kernel without an upper bound)
-WIDENED_OPS = {"ClampMinFwdOp", "GLADecodeOp", "MishFwdOp"}
+WIDENED_OPS = {"BitwiseNotFwdOp", "ClampMinFwdOp", "GLADecodeOp", "MishFwdOp"}
 
 
 def test_manifest_holds_the_hot_path_ops():
@@ -137,6 +137,7 @@ def test_manifest_roofline_pinned(op, label, dtype, flops, nbytes):
 
 def _static_ops():
     from tileops.ops.attention.multi_head_attention import MultiHeadAttentionFwdOp
+    from tileops.ops.elementwise.bitwise_not import BitwiseNotFwdOp
     from tileops.ops.elementwise.clamp_min import ClampMinFwdOp
     from tileops.ops.elementwise.clamp_scalar import ClampScalarFwdOp
     from tileops.ops.elementwise.gelu_and_mul import GeluAndMulFwdOp
@@ -167,6 +168,7 @@ def _static_ops():
         "HardsigmoidFwdOp": flat(HardsigmoidFwdOp),
         "ClampScalarFwdOp": flat(ClampScalarFwdOp),
         "ClampMinFwdOp": flat(ClampMinFwdOp),
+        "BitwiseNotFwdOp": flat(BitwiseNotFwdOp),
         "IsnanFwdOp": flat(IsnanFwdOp),
         "MishFwdOp": flat(MishFwdOp),
         "IsinfFwdOp": flat(IsinfFwdOp),

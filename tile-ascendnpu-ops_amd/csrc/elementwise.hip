@@ -369,6 +369,47 @@ static int dispatch_gated_gelu(int approx, const void* x, void* y, int64_t M, in
 
 using namespace tileops;
 
+// ---------------------------------------------------------------------------
+// Bitwise NOT (torch.bitwise_not) on the bytes of bool / integer tensors: every
+// integer type is its bytes complemented, a bool (one byte, 0 or 1) its byte
+// XOR 1.  16-byte non-temporal packs, then single bytes for the tail.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bitnot_vec_kernel(const u32x4* __restrict__ x,
+                                                         u32x4* __restrict__ y, int64_t npack,
+                                                         uint32_t mask) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= npack) return;
+  u32x4 v = __builtin_nontemporal_load(x + i);
+  v ^= u32x4{mask, mask, mask, mask};
+  __builtin_nontemporal_store(v, y + i);
+}
+
+__global__ __launch_bounds__(256) void bitnot_byte_kernel(const uint8_t* __restrict__ x,
+                                                          uint8_t* __restrict__ y, int64_t begin,
+                                                          int64_t n, uint32_t mask) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = (uint8_t)(x[i] ^ (uint8_t)mask);
+}
+
+extern "C" int tileops_bitwise_not_fwd(const void* x, void* y, int64_t nbytes, int is_bool,
+                                       void* stream) {
+  if (nbytes < 0) return TILEOPS_ESHAPE;
+  if (nbytes == 0) return 0;
+  if (!x || !y) return TILEOPS_ENULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t mask = is_bool ? 0x01010101u : 0xFFFFFFFFu;
+  const int64_t npack = (host_aligned16(x) && host_aligned16(y)) ? nbytes / 16 : 0;
+  if (npack > 0)
+    bitnot_vec_kernel<<<dim3((unsigned)((npack + 255) / 256)), dim3(256), 0, s>>>(
+        static_cast<const u32x4*>(x), static_cast<u32x4*>(y), npack, mask);
+  const int64_t done = npack * 16;
+  if (done < nbytes)
+    bitnot_byte_kernel<<<dim3((unsigned)stream_grid(nbytes - done, 256)), dim3(256), 0, s>>>(
+        static_cast<const uint8_t*>(x), static_cast<uint8_t*>(y), done, nbytes, mask);
+  return launch_status();
+}
+
 extern "C" int tileops_unary_fwd(int op, const void* x, void* y, int64_t n, int dtype, float lo,
                                  float hi, int flags, void* stream) {
   if (n < 0) return TILEOPS_ESHAPE;

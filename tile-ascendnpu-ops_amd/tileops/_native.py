@@ -77,6 +77,7 @@ SIGNATURES = {
         ctypes.c_size_t,
         [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64],
     ),
+    "tileops_bitwise_not_fwd": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
     "tileops_gla_decode_fwd": (
         _c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float,

@@ -1,3 +1,4 @@
+from tileops.kernels.elementwise.bitwise_not import BitwiseNotFwdKernel
 from tileops.kernels.elementwise.clamp_scalar import ClampScalarFwdKernel
 from tileops.kernels.elementwise.gelu_and_mul import GeluAndMulFwdKernel
 from tileops.kernels.elementwise.gelu_tanh_and_mul import GeluTanhAndMulFwdKernel
@@ -9,6 +10,7 @@ from tileops.kernels.elementwise.isnan import IsnanFwdKernel
 from tileops.kernels.elementwise.mish import MishFwdKernel
 
 __all__ = [
+    "BitwiseNotFwdKernel",
     "ClampScalarFwdKernel",
     "GeluAndMulFwdKernel",
     "GeluTanhAndMulFwdKernel",

@@ -1,3 +1,4 @@
+from tileops.ops.elementwise.bitwise_not import BitwiseNotFwdOp
 from tileops.ops.elementwise.clamp_min import ClampMinFwdOp
 from tileops.ops.elementwise.clamp_scalar import ClampScalarFwdOp
 from tileops.ops.elementwise.gelu_and_mul import GeluAndMulFwdOp
@@ -10,6 +11,7 @@ from tileops.ops.elementwise.isnan import IsnanFwdOp
 from tileops.ops.elementwise.mish import MishFwdOp
 
 __all__ = [
+    "BitwiseNotFwdOp",
     "ClampMinFwdOp",
     "ClampScalarFwdOp",
     "GeluAndMulFwdOp",

@@ -32,6 +32,23 @@ class HardswishWorkload(ShapedRandnWorkload):
     """Input of HardswishFwdOp."""
 
 
+class BitwiseNotWorkload(WorkloadBase):
+    """Input of BitwiseNotFwdOp: random bits of the dtype (bool: 0 / 1)."""
+
+    def __init__(self, shape: tuple, dtype: torch.dtype):
+        self.shape = tuple(shape)
+        self.dtype = dtype
+        self.n_total = prod(self.shape)
+
+    def gen_inputs(self):
+        dev = get_device_backend().name
+        if self.dtype == torch.bool:
+            return (torch.randint(0, 2, self.shape, device=dev).to(torch.bool),)
+        nbytes = self.n_total * torch.empty(0, dtype=self.dtype).element_size()
+        raw = torch.randint(0, 256, (nbytes,), device=dev, dtype=torch.uint8)
+        return (raw.view(self.dtype).reshape(self.shape),)
+
+
 class MishWorkload(ShapedRandnWorkload):
     """Input of MishFwdOp: randn of the workload shape."""
 
