@@ -374,6 +374,8 @@ using namespace tileops;
 // integer type is its bytes complemented, a bool (one byte, 0 or 1) its byte
 // XOR 1.  16-byte non-temporal packs, then single bytes for the tail.
 // ---------------------------------------------------------------------------
+namespace tileops {
+
 __global__ __launch_bounds__(256) void bitnot_vec_kernel(const u32x4* __restrict__ x,
                                                          u32x4* __restrict__ y, int64_t npack,
                                                          uint32_t mask) {
@@ -391,6 +393,8 @@ __global__ __launch_bounds__(256) void bitnot_byte_kernel(const uint8_t* __restr
   for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     y[i] = (uint8_t)(x[i] ^ (uint8_t)mask);
 }
+
+}  // namespace tileops
 
 extern "C" int tileops_bitwise_not_fwd(const void* x, void* y, int64_t nbytes, int is_bool,
                                        void* stream) {
