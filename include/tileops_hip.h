@@ -94,6 +94,21 @@ int tileops_unary_fwd(int op, const void* x, void* y, int64_t n, int dtype,
 int tileops_bitwise_not_fwd(const void* x, void* y, int64_t nbytes, int is_bool, void* stream);
 
 /*
+ * y = a + alpha * b with broadcasting (torch.add; torch.sub passes -alpha),
+ * computed in fp32 and rounded once to `dtype` (F32 / F16 / BF16).  The
+ * output is contiguous with `ndim` (<= 8) dimensions `out_shape`; a and b
+ * are read at element strides `a_strides` / `b_strides` per output
+ * dimension (0 on a broadcast dimension), host arrays of `ndim` entries.
+ * Replaces AddFwdKernel.forward / SubFwdKernel.forward
+ * (tileops/kernels/elementwise/add, sub; op interfaces
+ * tileops/ops/elementwise/add.py:61-155, sub.py), which materialised the
+ * broadcast with expand().contiguous() first.
+ */
+int tileops_add_fwd(const void* a, const void* b, void* y, int ndim, const int64_t* out_shape,
+                    const int64_t* a_strides, const int64_t* b_strides, float alpha, int dtype,
+                    void* stream);
+
+/*
  * y[i] = pred(x[i]) as one byte 0/1 (torch.bool storage), i < n.
  * Replaces IsnanFwdKernel.forward (tileops/kernels/elementwise/isnan/isnan.py:142-156),
  * IsinfFwdKernel.forward (tileops/kernels/elementwise/isinf/isinf.py:150) and

@@ -81,6 +81,18 @@ def hardsigmoid(x: np.ndarray, dtype: str) -> np.ndarray:
     return round_to(dtype, t / np.float32(6))
 
 
+def add(a: np.ndarray, b: np.ndarray, alpha, dtype: str) -> np.ndarray:
+    """torch.add(a, b, alpha=alpha) for half / fp32 storage: numpy broadcasting,
+    fp32 opmath fma(alpha, b, a) -- torch's CPU kernel fuses the multiply-add --
+    then rounded to the storage dtype (torch.sub is alpha -> -alpha).  The fma is
+    the fp64 sum of the exact fp64 product (a 24x24-bit product fits in 53 bits)
+    rounded to fp32."""
+    a64 = np.asarray(a, np.float32).astype(np.float64)
+    b64 = np.asarray(b, np.float32).astype(np.float64)
+    y = a64 + np.float64(np.float32(alpha)) * b64
+    return round_to(dtype, y.astype(np.float32))
+
+
 def bitwise_not(x: np.ndarray) -> np.ndarray:
     """torch.bitwise_not(x) (tests/ops/test_bitwise_not.py of the reference):
     the complement of every integer, logical NOT of a bool."""

@@ -26,7 +26,8 @@ HOT_PATH_OPS = {
     "LogSumExpFwdOp", "ArgmaxFwdOp", "MultiHeadAttentionFwdOp", "GatedDeltaNetPrefillFwdOp",
 }
 # ops beyond the hot path built on its kernels (the clamp kernel without an upper bound)
-WIDENED_OPS = {"BitwiseNotFwdOp", "ClampMinFwdOp", "GLADecodeOp", "MishFwdOp"}
+WIDENED_OPS = {"AddFwdOp", "BitwiseNotFwdOp", "ClampMinFwdOp", "GLADecodeOp", "MishFwdOp",
+               "SubFwdOp"}
 
 
 def test_manifest_holds_the_hot_path_ops():

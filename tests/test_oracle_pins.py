@@ -207,6 +207,24 @@ def test_argmax_other_axis_and_flat():
     assert orc.argreduce(x.reshape(1, -1), -1)[0] == torch.from_numpy(x).argmax().item()
 
 
+def test_add_matches_torch():
+    rng = np.random.default_rng(4)
+    for sa, sb in (((6, 5), (6, 5)), ((4, 1, 3), (2, 1)), ((7,), ())):
+        a = rng.standard_normal(sa).astype(np.float32)
+        b = rng.standard_normal(sb).astype(np.float32)
+        for dt, tdt in (("float32", torch.float32), ("float16", torch.float16),
+                        ("bfloat16", torch.bfloat16)):
+            ad, bd = orc.round_to(dt, a), orc.round_to(dt, b)
+            ta, tb = torch.from_numpy(ad).to(tdt), torch.from_numpy(np.asarray(bd)).to(tdt)
+            # the reference's golden: torch.add(a.float(), b.float(), alpha).to(dtype)
+            # (tests/ops/test_add.py:68-69), torch.sub likewise
+            for alpha in (1, 0.5, 3):
+                want = torch.add(ta.float(), tb.float(), alpha=alpha).to(tdt).float().numpy()
+                np.testing.assert_array_equal(orc.add(ad, bd, alpha, dt), want)
+                want = torch.sub(ta.float(), tb.float(), alpha=alpha).to(tdt).float().numpy()
+                np.testing.assert_array_equal(orc.add(ad, bd, -alpha, dt), want)
+
+
 def test_mish_matches_torch():
     x = np.concatenate([np.linspace(-30, 30, 4001), [0.0, -0.0, 60.0, -60.0, 100.0, -100.0,
                                                       np.inf, -np.inf, np.nan]]).astype(np.float32)

@@ -396,6 +396,112 @@ __global__ __launch_bounds__(256) void bitnot_byte_kernel(const uint8_t* __restr
 
 }  // namespace tileops
 
+namespace tileops {
+
+// ---------------------------------------------------------------------------
+// y = a + alpha * b (torch.add; torch.sub is alpha -> -alpha, exact), one fp32 fma
+// opmath rounded once.  Same-shape contiguous operands stream as 16-byte
+// packs; broadcast operands are read through per-dimension strides (0 on a
+// broadcast dimension) of the output's multi-index, with no materialised
+// copy.
+// ---------------------------------------------------------------------------
+constexpr int kMaxDims = 8;
+struct BcastDesc {
+  int ndim;
+  int64_t shape[kMaxDims];  // output shape
+  int64_t as[kMaxDims];     // element strides of a (0: broadcast)
+  int64_t bs[kMaxDims];     // element strides of b
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void add_vec_kernel(const T* __restrict__ a,
+                                                      const T* __restrict__ b, T* __restrict__ y,
+                                                      int64_t npack, float alpha) {
+  constexpr int V = Elem<T>::kVec;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= npack) return;
+  const Pack<T> pa = load_pack_nt(a + i * V), pb = load_pack_nt(b + i * V);
+  Pack<T> out;
+#pragma unroll
+  for (int e = 0; e < V; ++e)
+    out.v[e] = Elem<T>::from_f32(fmaf(alpha, Elem<T>::to_f32(pb.v[e]), Elem<T>::to_f32(pa.v[e])));
+  store_pack_nt(y + i * V, out);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void add_bcast_kernel(const T* __restrict__ a,
+                                                        const T* __restrict__ b,
+                                                        T* __restrict__ y, int64_t begin,
+                                                        int64_t n, float alpha, BcastDesc d) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, ao = 0, bo = 0;
+    for (int k = d.ndim - 1; k >= 0; --k) {
+      const int64_t idx = rem % d.shape[k];
+      rem /= d.shape[k];
+      ao += idx * d.as[k];
+      bo += idx * d.bs[k];
+    }
+    y[i] = Elem<T>::from_f32(fmaf(alpha, Elem<T>::to_f32(b[bo]), Elem<T>::to_f32(a[ao])));
+  }
+}
+
+template <typename T>
+static int launch_add(const void* av, const void* bv, void* yv, const BcastDesc& d, int64_t n,
+                      float alpha, hipStream_t s) {
+  const T* a = static_cast<const T*>(av);
+  const T* b = static_cast<const T*>(bv);
+  T* y = static_cast<T*>(yv);
+  constexpr int V = Elem<T>::kVec;
+  bool flat = true;  // both operands contiguous over the whole output
+  int64_t expect = 1;
+  for (int k = d.ndim - 1; k >= 0; --k) {
+    if (d.shape[k] != 1 && (d.as[k] != expect || d.bs[k] != expect)) flat = false;
+    expect *= d.shape[k];
+  }
+  int64_t npack = 0;
+  if (flat && host_aligned16(a) && host_aligned16(b) && host_aligned16(y)) {
+    npack = n / V;
+    if (npack > 0)
+      add_vec_kernel<T><<<dim3((unsigned)((npack + 255) / 256)), dim3(256), 0, s>>>(a, b, y, npack,
+                                                                                  alpha);
+  }
+  const int64_t done = npack * V;
+  if (done < n)
+    add_bcast_kernel<T><<<dim3((unsigned)stream_grid(n - done, 256)), dim3(256), 0, s>>>(
+        a, b, y, done, n, alpha, d);
+  return launch_status();
+}
+
+}  // namespace tileops
+
+extern "C" int tileops_add_fwd(const void* a, const void* b, void* y, int ndim,
+                               const int64_t* out_shape, const int64_t* a_strides,
+                               const int64_t* b_strides, float alpha, int dtype, void* stream) {
+  if (ndim < 0 || ndim > kMaxDims) return TILEOPS_ESHAPE;
+  if (ndim > 0 && (!out_shape || !a_strides || !b_strides)) return TILEOPS_ENULL;
+  BcastDesc d{};
+  d.ndim = ndim;
+  int64_t n = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (out_shape[k] < 0) return TILEOPS_ESHAPE;
+    if (a_strides[k] < 0 || b_strides[k] < 0) return TILEOPS_EINVAL;
+    d.shape[k] = out_shape[k];
+    d.as[k] = a_strides[k];
+    d.bs[k] = b_strides[k];
+    n *= out_shape[k];
+  }
+  if (dtype < TILEOPS_F32 || dtype > TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (n == 0) return 0;
+  if (!a || !b || !y) return TILEOPS_ENULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TILEOPS_F32: return launch_add<float>(a, b, y, d, n, alpha, s);
+    case TILEOPS_F16: return launch_add<f16>(a, b, y, d, n, alpha, s);
+    default: return launch_add<bf16>(a, b, y, d, n, alpha, s);
+  }
+}
+
 extern "C" int tileops_bitwise_not_fwd(const void* x, void* y, int64_t nbytes, int is_bool,
                                        void* stream) {
   if (nbytes < 0) return TILEOPS_ESHAPE;

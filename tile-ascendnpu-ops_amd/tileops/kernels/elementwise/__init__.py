@@ -1,3 +1,4 @@
+from tileops.kernels.elementwise.add import AddFwdKernel, SubFwdKernel
 from tileops.kernels.elementwise.bitwise_not import BitwiseNotFwdKernel
 from tileops.kernels.elementwise.clamp_scalar import ClampScalarFwdKernel
 from tileops.kernels.elementwise.gelu_and_mul import GeluAndMulFwdKernel
@@ -10,7 +11,9 @@ from tileops.kernels.elementwise.isnan import IsnanFwdKernel
 from tileops.kernels.elementwise.mish import MishFwdKernel
 
 __all__ = [
+    "AddFwdKernel",
     "BitwiseNotFwdKernel",
+    "SubFwdKernel",
     "ClampScalarFwdKernel",
     "GeluAndMulFwdKernel",
     "GeluTanhAndMulFwdKernel",

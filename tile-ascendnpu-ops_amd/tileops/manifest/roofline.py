@@ -21,6 +21,13 @@ from tileops.manifest import WORKLOAD_RESERVED_KEYS, load_manifest
 __all__ = ["manifest_roofline", "reduced_dims"]
 
 
+def _broadcast(*shapes) -> tuple:
+    """The broadcast shape of ``shapes`` (PyTorch / numpy rules)."""
+    import numpy as np
+
+    return tuple(np.broadcast_shapes(*(tuple(s) for s in shapes)))
+
+
 def _product(values: Iterable[int]) -> int:
     return int(math.prod(int(v) for v in values))
 
@@ -39,6 +46,7 @@ def reduced_dims(shape, dim) -> list[int]:
 _SAFE = {
     "__builtins__": {},
     "product": _product,
+    "broadcast": _broadcast,
     "reduced_dims": reduced_dims,
     "range": range,
     "len": len,

@@ -1,3 +1,4 @@
+from tileops.ops.elementwise.add import AddFwdOp, SubFwdOp
 from tileops.ops.elementwise.bitwise_not import BitwiseNotFwdOp
 from tileops.ops.elementwise.clamp_min import ClampMinFwdOp
 from tileops.ops.elementwise.clamp_scalar import ClampScalarFwdOp
@@ -11,7 +12,9 @@ from tileops.ops.elementwise.isnan import IsnanFwdOp
 from tileops.ops.elementwise.mish import MishFwdOp
 
 __all__ = [
+    "AddFwdOp",
     "BitwiseNotFwdOp",
+    "SubFwdOp",
     "ClampMinFwdOp",
     "ClampScalarFwdOp",
     "GeluAndMulFwdOp",

@@ -32,6 +32,22 @@ class HardswishWorkload(ShapedRandnWorkload):
     """Input of HardswishFwdOp."""
 
 
+class BinaryWorkload(WorkloadBase):
+    """Operands of AddFwdOp / SubFwdOp: two randn tensors of their own shapes
+    (broadcast together by the op)."""
+
+    def __init__(self, input_shape: tuple, other_shape: tuple, dtype: torch.dtype):
+        self.input_shape = tuple(input_shape)
+        self.other_shape = tuple(other_shape)
+        self.dtype = dtype
+        self.n_total = prod(torch.broadcast_shapes(self.input_shape, self.other_shape))
+
+    def gen_inputs(self):
+        dev = get_device_backend().name
+        return (torch.randn(self.input_shape, device=dev).to(self.dtype),
+                torch.randn(self.other_shape, device=dev).to(self.dtype))
+
+
 class BitwiseNotWorkload(WorkloadBase):
     """Input of BitwiseNotFwdOp: random bits of the dtype (bool: 0 / 1)."""
 
