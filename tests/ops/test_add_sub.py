@@ -22,6 +22,9 @@ SHAPES = [
     ((1024, 4096), (1, 4096)),
     ((3, 1, 77), (5, 1)),        # both operands broadcast, ragged
     ((7,), ()),                  # scalar operand
+    ((64,), ()),                 # scalar operand, whole packs
+    ((1, 64), (32, 64)),         # the first operand broadcast
+    ((4, 8, 1, 32), (8, 32, 1)),  # rows of one operand, columns of the other
 ]
 
 

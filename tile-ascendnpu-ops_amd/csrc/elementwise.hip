@@ -446,13 +446,120 @@ __global__ __launch_bounds__(256) void add_bcast_kernel(const T* __restrict__ a,
   }
 }
 
+// Broadcast operands whose innermost dimension is unit-stride or broadcast
+// (bias rows, per-channel scales): a thread takes one 16-byte pack of an output
+// row, so the outer multi-index is computed once per pack rather than per
+// element, in 32-bit arithmetic (I = uint32_t) when every offset fits.  A
+// broadcast operand (some stride 0) is re-read across rows and keeps the
+// cached load; a streamed one takes the non-temporal load.
+template <typename T, typename I>
+__global__ __launch_bounds__(256) void add_inner_kernel(const T* __restrict__ a,
+                                                        const T* __restrict__ b,
+                                                        T* __restrict__ y, I npack, I row_packs,
+                                                        float alpha, BcastDesc d, int a_bc,
+                                                        int b_bc) {
+  constexpr int V = Elem<T>::kVec;
+  const int nd = d.ndim;  // >= 1; dimension nd - 1 is the row
+  const bool a_vec = d.as[nd - 1] != 0, b_vec = d.bs[nd - 1] != 0;
+  const I stride = (I)gridDim.x * blockDim.x;
+  for (I p = (I)blockIdx.x * blockDim.x + threadIdx.x; p < npack; p += stride) {
+    I r = p / row_packs;
+    const I c = (p - r * row_packs) * V;
+    I ao = a_vec ? c : 0, bo = b_vec ? c : 0;
+    for (int k = nd - 2; k >= 0; --k) {
+      const I sh = (I)d.shape[k], q = r / sh, idx = r - q * sh;
+      r = q;
+      ao += idx * (I)d.as[k];
+      bo += idx * (I)d.bs[k];
+    }
+    Pack<T> pa, pb, out;
+    if (a_vec) {
+      pa = a_bc ? load_pack(a + ao) : load_pack_nt(a + ao);
+    } else {
+      const T v = a[ao];
+#pragma unroll
+      for (int e = 0; e < V; ++e) pa.v[e] = v;
+    }
+    if (b_vec) {
+      pb = b_bc ? load_pack(b + bo) : load_pack_nt(b + bo);
+    } else {
+      const T v = b[bo];
+#pragma unroll
+      for (int e = 0; e < V; ++e) pb.v[e] = v;
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      out.v[e] = Elem<T>::from_f32(fmaf(alpha, Elem<T>::to_f32(pb.v[e]), Elem<T>::to_f32(pa.v[e])));
+    store_pack_nt(y + (int64_t)p * V, out);
+  }
+}
+
+// Drops size-1 dimensions and merges a dimension into the one outside it
+// where both operands' strides chain (stride[k-1] == stride[k] * shape[k],
+// broadcast dimensions included), so the index arithmetic runs over as few
+// dimensions as the layout allows.
+static void coalesce_dims(BcastDesc& d) {
+  BcastDesc o{};
+  int m = 0;
+  for (int k = 0; k < d.ndim; ++k) {
+    if (d.shape[k] == 1) continue;
+    if (m > 0 && o.as[m - 1] == d.as[k] * d.shape[k] && o.bs[m - 1] == d.bs[k] * d.shape[k]) {
+      o.shape[m - 1] *= d.shape[k];
+      o.as[m - 1] = d.as[k];
+      o.bs[m - 1] = d.bs[k];
+    } else {
+      o.shape[m] = d.shape[k];
+      o.as[m] = d.as[k];
+      o.bs[m] = d.bs[k];
+      ++m;
+    }
+  }
+  o.ndim = m;
+  d = o;
+}
+
+// The pack kernel applies when the row length is a whole number of packs,
+// each operand's row is unit-stride (16-byte aligned base and row offsets) or
+// broadcast, and the output is 16-byte aligned.  Returns false otherwise.
 template <typename T>
-static int launch_add(const void* av, const void* bv, void* yv, const BcastDesc& d, int64_t n,
+static bool launch_add_inner(const T* a, const T* b, T* y, const BcastDesc& d, int64_t n,
+                             float alpha, hipStream_t s) {
+  constexpr int V = Elem<T>::kVec;
+  const int nd = d.ndim;
+  if (nd < 1 || d.shape[nd - 1] % V != 0 || !host_aligned16(y)) return false;
+  int64_t amax = 0, bmax = 0;
+  bool a_bc = false, b_bc = false;
+  for (int k = 0; k < nd; ++k) {
+    amax += (d.shape[k] - 1) * d.as[k];
+    bmax += (d.shape[k] - 1) * d.bs[k];
+    a_bc |= d.as[k] == 0;
+    b_bc |= d.bs[k] == 0;
+  }
+  const int64_t ain = d.as[nd - 1], bin = d.bs[nd - 1];
+  if ((ain != 0 && ain != 1) || (bin != 0 && bin != 1)) return false;
+  for (int k = 0; k < nd - 1; ++k)
+    if ((ain && d.as[k] % V) || (bin && d.bs[k] % V)) return false;
+  if ((ain && !host_aligned16(a)) || (bin && !host_aligned16(b))) return false;
+  const int64_t npack = n / V, row_packs = d.shape[nd - 1] / V;
+  const unsigned grid = (unsigned)stream_grid(npack, 256);
+  if (npack < (int64_t)UINT32_MAX - (int64_t)grid * 256 && amax < (int64_t)UINT32_MAX &&
+      bmax < (int64_t)UINT32_MAX)
+    add_inner_kernel<T, uint32_t><<<dim3(grid), dim3(256), 0, s>>>(
+        a, b, y, (uint32_t)npack, (uint32_t)row_packs, alpha, d, a_bc, b_bc);
+  else
+    add_inner_kernel<T, int64_t><<<dim3(grid), dim3(256), 0, s>>>(a, b, y, npack, row_packs,
+                                                                   alpha, d, a_bc, b_bc);
+  return true;
+}
+
+template <typename T>
+static int launch_add(const void* av, const void* bv, void* yv, BcastDesc d, int64_t n,
                       float alpha, hipStream_t s) {
   const T* a = static_cast<const T*>(av);
   const T* b = static_cast<const T*>(bv);
   T* y = static_cast<T*>(yv);
   constexpr int V = Elem<T>::kVec;
+  coalesce_dims(d);
   bool flat = true;  // both operands contiguous over the whole output
   int64_t expect = 1;
   for (int k = d.ndim - 1; k >= 0; --k) {
@@ -460,6 +567,7 @@ static int launch_add(const void* av, const void* bv, void* yv, const BcastDesc&
     expect *= d.shape[k];
   }
   int64_t npack = 0;
+  if (!flat && launch_add_inner<T>(a, b, y, d, n, alpha, s)) return launch_status();
   if (flat && host_aligned16(a) && host_aligned16(b) && host_aligned16(y)) {
     npack = n / V;
     if (npack > 0)
