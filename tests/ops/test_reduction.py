@@ -102,15 +102,36 @@ def test_logsumexp_1d_and_multidim(dtype):
 
 
 @pytest.mark.gpu
-def test_logsumexp_special_rows():
-    x = torch.randn(64, 4096, device="cuda") * 2
+@pytest.mark.parametrize("rows", [64, 8192])  # 4 wavefronts per row / 1 per row
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_logsumexp_special_rows(rows, dtype):
+    # Finite maxima beyond 2e38 (up to the dtype's largest finite value) must
+    # stay finite, as torch.logsumexp keeps them: shift by the max unless it
+    # is infinite.
+    big = torch.finfo(dtype).max
+    x = torch.randn(rows, 4096, device="cuda") * 2
     x[0] = float("-inf")
     x[1, 17] = float("inf")
     x[2, 4000] = float("nan")
     x[3] = 1e30
     x[4, :100] = float("-inf")
-    y = LogSumExpFwdOp(dtype=torch.float32)(x)
-    assert_close_np(to_np(y), orc.logsumexp(to_np(x), "float32"), 1e-5, 1e-5, "lse special")
+    x[5, 7] = 3e38
+    x[6] = -3e38
+    x[7] = big
+    x[8] = -big
+    x[9, :2048] = -3e38
+    x[9, 2048:] = float("-inf")
+    x[10, 5] = float("inf")
+    x[10, 6] = float("-inf")
+    x[10, 7] = 3e38
+    x[11, 3000] = 3e38
+    x[11, 3001] = float("nan")
+    x = x.to(dtype)
+    y = LogSumExpFwdOp(dtype=dtype)(x)
+    ref = orc.logsumexp(to_np(x), NAMES[dtype])
+    assert np.isfinite(ref[[3, 5, 6, 7, 8, 9]]).all()
+    atol, rtol = ref_tolerance(dtype)
+    assert_close_np(to_np(y), ref, atol, rtol, "lse special")
 
 
 @pytest.mark.smoke

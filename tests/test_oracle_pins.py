@@ -184,6 +184,19 @@ def test_logsumexp_matches_torch(dtype):
                - (2.0 + math.log(300))) < 1e-6
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_logsumexp_huge_finite_rows(dtype):
+    # finite maxima near the top of the range stay finite, as in torch
+    big = float(torch.finfo(DTYPES[dtype]).max)
+    rows = [[3e38, 0.0, 1.0], [-3e38, -3e38, -3e38], [big, big, 0.0], [-big, -big, -big],
+            [3e38, -np.inf, np.inf], [-3e38, -np.inf, -np.inf], [3e38, np.nan, 1.0]]
+    x = _as_storage(np.array(rows, np.float32), dtype)
+    ref = torch.logsumexp(torch.from_numpy(x), dim=-1).to(DTYPES[dtype]).float().numpy()
+    got = orc.logsumexp(x, dtype)
+    assert np.isfinite(got[[0, 1, 2, 3, 5]]).all() and got[4] == np.inf and np.isnan(got[6])
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=0)
+
+
 @pytest.mark.parametrize("is_min", [False, True])
 def test_argreduce_matches_torch(is_min):
     rng = np.random.default_rng(4)
@@ -223,6 +236,61 @@ def test_add_matches_torch():
                 np.testing.assert_array_equal(orc.add(ad, bd, alpha, dt), want)
                 want = torch.sub(ta.float(), tb.float(), alpha=alpha).to(tdt).float().numpy()
                 np.testing.assert_array_equal(orc.add(ad, bd, -alpha, dt), want)
+
+
+def _ulp_diff32(x, y):
+    xi = np.asarray(x, np.float32).view(np.int32).astype(np.int64)
+    yi = np.asarray(y, np.float32).view(np.int32).astype(np.int64)
+    xi = np.where(xi < 0, -(xi & 0x7FFFFFFF), xi)
+    yi = np.where(yi < 0, -(yi & 0x7FFFFFFF), yi)
+    return np.abs(xi - yi)
+
+
+def test_lerp_matches_torch():
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((64, 257)).astype(np.float32)
+    b = (rng.standard_normal((64, 257)) * 3).astype(np.float32)
+    wt = rng.uniform(-1.5, 2.5, (64, 257)).astype(np.float32)
+    for dt, tdt in (("float32", torch.float32), ("float16", torch.float16),
+                    ("bfloat16", torch.bfloat16)):
+        ad, bd, wd = orc.round_to(dt, a), orc.round_to(dt, b), orc.round_to(dt, wt)
+        ta, tb, tw = (torch.from_numpy(v).to(tdt) for v in (ad, bd, wd))
+        # the reference's golden is torch.lerp on the storage dtype
+        for w in (0.0, 0.3, 0.5, 0.7, 1.0, -1.5, 2.0):
+            want = torch.lerp(ta, tb, w).float().numpy()
+            got = orc.lerp(ad, bd, w, dt)
+            if dt == "float32":
+                assert _ulp_diff32(got, want).max() <= 1
+            else:
+                np.testing.assert_array_equal(got, want)
+        want = torch.lerp(ta, tb, tw).float().numpy()
+        got = orc.lerp(ad, bd, wd, dt)
+        if dt == "float32":
+            assert _ulp_diff32(got, want).max() <= 1
+        else:
+            np.testing.assert_array_equal(got, want)
+    # broadcasting, as torch broadcasts
+    a1 = rng.standard_normal((4, 1, 8)).astype(np.float32)
+    b1 = rng.standard_normal((3, 1)).astype(np.float32)
+    want = torch.lerp(torch.from_numpy(a1), torch.from_numpy(b1), 0.3).numpy()
+    assert orc.lerp(a1, b1, 0.3, "float32").shape == want.shape == (4, 3, 8)
+    assert _ulp_diff32(orc.lerp(a1, b1, 0.3, "float32"), want).max() <= 1
+
+
+def test_lerp_closed_forms():
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal(1000).astype(np.float32)
+    b = rng.standard_normal(1000).astype(np.float32)
+    # the endpoints are exact, whichever side of the formula computes them
+    np.testing.assert_array_equal(orc.lerp(a, b, 0.0, "float32"), a)
+    np.testing.assert_array_equal(orc.lerp(a, b, 1.0, "float32"), b)
+    # the midpoint of two small integers is exact
+    ia, ib = np.float32([1, -3, 8]), np.float32([4, 5, -2])
+    np.testing.assert_array_equal(orc.lerp(ia, ib, 0.5, "float32"), (ia + ib) / 2)
+    # a == b is a fixed point for every weight, and NaN propagates
+    np.testing.assert_array_equal(orc.lerp(a, a, 0.37, "float32"), a)
+    out = orc.lerp(np.float32([np.nan, 1.0]), np.float32([1.0, np.nan]), 0.25, "float32")
+    assert np.isnan(out).all()
 
 
 def test_mish_matches_torch():

@@ -18,31 +18,37 @@ constexpr float kLog2e = 1.4426950408889634f;
 // ---------------------------------------------------------------------------
 // LogSumExp: online (max, scaled-sum) per lane.
 //
-// The running max is clamped to [-kBig, kBig], which reproduces
-// torch.logsumexp's special cases without per-element tests (x - m is
-// +-inf exactly when x is, and m - m' never produces inf - inf):
-//   all -inf    -> sum 0, log 0 = -inf          (result -inf)
-//   any +inf    -> exp(+inf - kBig) = +inf      (result +inf)
-//   any NaN     -> NaN enters the sum           (result NaN)
+// m is the running max of everything folded so far (NaN never wins the
+// compare, so m stays in [-inf, +inf]); s = sum exp(x - shift(m)) where
+// shift(m) = m for a finite max and 0 for an infinite one, as torch does.
+// That reproduces torch.logsumexp's special cases and keeps every finite
+// max up to FLT_MAX finite:
+//   all -inf    -> shift 0, s = 0, log 0 + 0 = -inf
+//   any +inf    -> shift 0, exp(+inf) = +inf in s   (result +inf)
+//   any NaN     -> NaN enters s                     (result NaN)
+// s == 0 exactly when m == -inf (a finite max contributes exp(0) = 1), and
+// such a sum is rescaled to 0 without evaluating a factor that could be
+// exp(+huge) = inf (0 * inf would be NaN).
 // ---------------------------------------------------------------------------
 struct LseState {
-  float m;  // running max, clamped to [-kBig, kBig]
-  float s;  // sum of exp(x - m)
+  float m;  // running max, -inf while nothing finite or +inf was folded
+  float s;  // sum of exp(x - lse_shift(m))
 };
 
-constexpr float kBig = 2.0e38f;  // kBig * log2(e) = 2.9e38 < FLT_MAX
+__device__ __forceinline__ float lse_shift(float m) {
+  return __builtin_fabsf(m) <= FLT_MAX ? m : 0.0f;
+}
 
-__device__ __forceinline__ float clampf_fin(float v) {
-  v = v > kBig ? kBig : v;
-  return v < -kBig ? -kBig : v;
+// s, taken relative to shift `from`, re-expressed relative to shift `to`.
+__device__ __forceinline__ float lse_rescale(float s, float from, float to) {
+  const float f = __builtin_amdgcn_exp2f((from - to) * kLog2e);
+  return s == 0.0f ? 0.0f : s * f;
 }
 
 __device__ __forceinline__ LseState lse_merge(LseState a, LseState b) {
   const float m = a.m > b.m ? a.m : b.m;
-  // exp2((a.m - m) * log2e) with both maxima finite
-  const float s = a.s * __builtin_amdgcn_exp2f((a.m - m) * kLog2e) +
-                  b.s * __builtin_amdgcn_exp2f((b.m - m) * kLog2e);
-  return {m, s};
+  const float sh = lse_shift(m);
+  return {m, lse_rescale(a.s, lse_shift(a.m), sh) + lse_rescale(b.s, lse_shift(b.m), sh)};
 }
 
 template <int CNT>
@@ -50,13 +56,14 @@ __device__ __forceinline__ void lse_fold(LseState& st, const float (&v)[CNT]) {
   float bm = v[0];
 #pragma unroll
   for (int i = 1; i < CNT; ++i) bm = v[i] > bm ? v[i] : bm;
-  const float mn = clampf_fin(bm > st.m ? bm : st.m);
+  const float mn = bm > st.m ? bm : st.m;
+  const float sh = lse_shift(mn);
   // exp(x - m) as exp2((x - m) * log2 e): subtracting first keeps the
   // exponent exact for large |m| (an fma(x, log2 e, -m log2 e) would leave
   // the rounding residue of m log2 e, ~1e31 at |m| ~ 1e38).
-  float acc = st.s * __builtin_amdgcn_exp2f((st.m - mn) * kLog2e);
+  float acc = lse_rescale(st.s, lse_shift(st.m), sh);
 #pragma unroll
-  for (int i = 0; i < CNT; ++i) acc += __builtin_amdgcn_exp2f((v[i] - mn) * kLog2e);
+  for (int i = 0; i < CNT; ++i) acc += __builtin_amdgcn_exp2f((v[i] - sh) * kLog2e);
   st.m = mn;
   st.s = acc;
 }
@@ -71,8 +78,8 @@ __device__ __forceinline__ LseState lse_wave(LseState st) {
 }
 
 __device__ __forceinline__ float lse_final(LseState st) {
-  // log(s) + m; s >= 1 whenever any finite element exists.
-  return logf(st.s) + st.m;
+  // log(s) + shift; s >= 1 whenever the max is finite.
+  return logf(st.s) + lse_shift(st.m);
 }
 
 // ---------------------------------------------------------------------------
@@ -126,7 +133,7 @@ template <> struct RowState<2> { typedef ArgState S; };
 
 template <int OP>
 __device__ __forceinline__ typename RowState<OP>::S row_init() {
-  if constexpr (OP == 0) return LseState{-kBig, 0.0f};
+  if constexpr (OP == 0) return LseState{-INFINITY, 0.0f};
   else return ArgState{0.0f, -1};
 }
 
