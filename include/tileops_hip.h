@@ -109,6 +109,25 @@ int tileops_add_fwd(const void* a, const void* b, void* y, int ndim, const int64
                     void* stream);
 
 /*
+ * y = lerp(a, b, weight) with broadcasting (torch.lerp): a + w (b - a) for
+ * |w| < 0.5, else b - (1 - w)(b - a), each an fp32 fma rounded once to
+ * `dtype` (F32 / F16 / BF16).  With `w` NULL the weight is the scalar
+ * `weight` (w_strides unused); otherwise the weight tensor `w` (same dtype)
+ * is read at `w_strides`.  Output, shapes and strides as tileops_add_fwd.
+ * Replaces LerpScalarFwdKernel.forward
+ * (tileops/kernels/elementwise/lerp_scalar/lerp_scalar.py:148; op interface
+ * tileops/ops/elementwise/lerp_scalar.py:38-157) and
+ * LerpTensorFwdKernel.forward
+ * (tileops/kernels/elementwise/lerp_tensor/lerp_tensor.py:170; op interface
+ * tileops/ops/elementwise/lerp_tensor.py:35-165), which materialised the
+ * broadcast with expand().contiguous() first.
+ */
+int tileops_lerp_fwd(const void* a, const void* b, const void* w, void* y, int ndim,
+                     const int64_t* out_shape, const int64_t* a_strides,
+                     const int64_t* b_strides, const int64_t* w_strides, float weight, int dtype,
+                     void* stream);
+
+/*
  * y[i] = pred(x[i]) as one byte 0/1 (torch.bool storage), i < n.
  * Replaces IsnanFwdKernel.forward (tileops/kernels/elementwise/isnan/isnan.py:142-156),
  * IsinfFwdKernel.forward (tileops/kernels/elementwise/isinf/isinf.py:150) and

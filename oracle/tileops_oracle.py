@@ -93,6 +93,28 @@ def add(a: np.ndarray, b: np.ndarray, alpha, dtype: str) -> np.ndarray:
     return round_to(dtype, y.astype(np.float32))
 
 
+def lerp(a: np.ndarray, b: np.ndarray, w, dtype: str) -> np.ndarray:
+    """torch.lerp(a, b, w) for half / fp32 storage (tests/ops/test_lerp_scalar.py:58-60,
+    test_lerp_tensor.py; the golden is torch.lerp itself): numpy broadcasting of
+    a, b and a scalar or array weight, fp32 opmath d = b - a (rounded to fp32),
+    then torch's two-sided form -- a + w d when |w| < 0.5, else b - (1 - w) d,
+    each side one fused multiply-add (torch's vectorised CPU kernel, and its
+    GPU kernel under contraction, fuse it) -- rounded to the storage dtype.
+    The fma is emulated as the fp64 sum of the exact fp64 product, rounded to
+    fp32 (it can differ from a true fma by one fp32 ulp in rare double-rounding
+    cases)."""
+    a32 = np.asarray(a, np.float32)
+    b32 = np.asarray(b, np.float32)
+    w32 = np.asarray(w, np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        d = (b32 - a32).astype(np.float32)
+        small = np.abs(w32) < np.float32(0.5)
+        coef = np.where(small, w32, (w32 - np.float32(1.0)).astype(np.float32))
+        base = np.where(small, a32, b32)
+        y = coef.astype(np.float64) * d.astype(np.float64) + base.astype(np.float64)
+    return round_to(dtype, y.astype(np.float32))
+
+
 def bitwise_not(x: np.ndarray) -> np.ndarray:
     """torch.bitwise_not(x) (tests/ops/test_bitwise_not.py of the reference):
     the complement of every integer, logical NOT of a bool."""

@@ -14,7 +14,8 @@ import torch
 
 from oracle import tileops_oracle as orc
 from tests._util import NAMES, assert_close_np, ref_tolerance, to_np
-from tileops.ops.elementwise.add import AddFwdOp, SubFwdOp
+from tileops.ops.elementwise.add import AddFwdOp
+from tileops.ops.elementwise.sub import SubFwdOp
 
 SHAPES = [
     ((2048, 4096), (2048, 4096)),
@@ -65,3 +66,24 @@ def test_add_sub_eval_roofline():
     n = 16 * 256 * 56 * 56
     assert op.eval_roofline() == (n, 3 * n * 2)
     assert SubFwdOp(input=(8,), other=(8,), dtype=torch.float32, alpha=2).eval_roofline() == (16, 96)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("op_cls, sign", [(AddFwdOp, 1.0), (SubFwdOp, -1.0)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_add_sub_storage_offset_operands(op_cls, sign, dtype):
+    # views that start one element into their storage are not 16-byte
+    # aligned: the kernels must take their element-wise paths for them
+    base = torch.randn(1 + 96 * 64, device="cuda").to(dtype)
+    a = base[1:].view(96, 64)                       # same shape, misaligned
+    b = torch.randn(96, 65, device="cuda").to(dtype)[:, 1:]  # row offset 1
+    for other, oshape in ((b, (96, 64)), (b[:1], (1, 64)), (b[:, :1], (96, 1))):
+        op = op_cls(input=(96, 64), other=oshape, dtype=dtype, alpha=0.5)
+        y = op(a, other)
+        want = orc.add(to_np(a), to_np(other), sign * 0.5, NAMES[dtype])
+        atol, rtol = ref_tolerance(dtype)
+        assert_close_np(to_np(y), want, atol, rtol, f"offset {op_cls.__name__} {oshape} {dtype}")
+    # the second operand misaligned against an aligned first one, flat
+    y = op_cls(input=(96 * 64,), other=(96 * 64,), dtype=dtype)(
+        torch.randn(96 * 64, device="cuda").to(dtype), base[1:])
+    assert y.shape == (96 * 64,)

@@ -26,8 +26,8 @@ HOT_PATH_OPS = {
     "LogSumExpFwdOp", "ArgmaxFwdOp", "MultiHeadAttentionFwdOp", "GatedDeltaNetPrefillFwdOp",
 }
 # ops beyond the hot path built on its kernels (the clamp kernel without an upper bound)
-WIDENED_OPS = {"AddFwdOp", "BitwiseNotFwdOp", "ClampMinFwdOp", "GLADecodeOp", "MishFwdOp",
-               "SubFwdOp"}
+WIDENED_OPS = {"AddFwdOp", "BitwiseNotFwdOp", "ClampMinFwdOp", "GLADecodeOp", "LerpFwdOp",
+               "LerpTensorFwdOp", "MishFwdOp", "SubFwdOp"}
 
 
 def test_manifest_holds_the_hot_path_ops():
@@ -138,6 +138,7 @@ def test_manifest_roofline_pinned(op, label, dtype, flops, nbytes):
 
 def _static_ops():
     from tileops.ops.attention.multi_head_attention import MultiHeadAttentionFwdOp
+    from tileops.ops.elementwise.add import AddFwdOp
     from tileops.ops.elementwise.bitwise_not import BitwiseNotFwdOp
     from tileops.ops.elementwise.clamp_min import ClampMinFwdOp
     from tileops.ops.elementwise.clamp_scalar import ClampScalarFwdOp
@@ -148,7 +149,10 @@ def _static_ops():
     from tileops.ops.elementwise.isfinite import IsfiniteFwdOp
     from tileops.ops.elementwise.isinf import IsinfFwdOp
     from tileops.ops.elementwise.isnan import IsnanFwdOp
+    from tileops.ops.elementwise.lerp_scalar import LerpFwdOp
+    from tileops.ops.elementwise.lerp_tensor import LerpTensorFwdOp
     from tileops.ops.elementwise.mish import MishFwdOp
+    from tileops.ops.elementwise.sub import SubFwdOp
     from tileops.ops.linear_attention.gdn_prefill import GatedDeltaNetPrefillFwdOp
     from tileops.ops.linear_attention.gla_decode import GLADecodeOp
 
@@ -181,6 +185,15 @@ def _static_ops():
             w.get("is_causal", True), dt),
         "GLADecodeOp": lambda w, dt: GLADecodeOp(w["B"], w["H"], w["DK"], w["DV"],
                                                  scale=w.get("scale", -1.0), dtype=dt),
+        "AddFwdOp": lambda w, dt: AddFwdOp(input=tuple(w["input_shape"]),
+                                           other=tuple(w["other_shape"]), dtype=dt),
+        "SubFwdOp": lambda w, dt: SubFwdOp(input=tuple(w["input_shape"]),
+                                           other=tuple(w["other_shape"]), dtype=dt),
+        "LerpFwdOp": lambda w, dt: LerpFwdOp(input=tuple(w["input_shape"]),
+                                             end=tuple(w["end_shape"]), dtype=dt),
+        "LerpTensorFwdOp": lambda w, dt: LerpTensorFwdOp(
+            input=tuple(w["input_shape"]), end=tuple(w["input_shape"]),
+            weight=tuple(w["input_shape"]), dtype=dt),
         "GatedDeltaNetPrefillFwdOp": lambda w, dt: GatedDeltaNetPrefillFwdOp(
             w["batch"], w["seq_len"], w["heads"], w["dim_k"], w["dim_v"], dtype=dt),
     }

@@ -6,7 +6,7 @@ import torch
 
 from tileops.benchmark.benchmark_base import BenchmarkReport, ManifestBenchmark
 from tileops.manifest import load_workloads
-from tileops.ops.elementwise.add import SubFwdOp
+from tileops.ops.elementwise.sub import SubFwdOp
 from tileops.workloads.elementwise import BinaryWorkload
 
 _OP = "SubFwdOp"

@@ -399,118 +399,154 @@ __global__ __launch_bounds__(256) void bitnot_byte_kernel(const uint8_t* __restr
 namespace tileops {
 
 // ---------------------------------------------------------------------------
-// y = a + alpha * b (torch.add; torch.sub is alpha -> -alpha, exact), one fp32 fma
-// opmath rounded once.  Same-shape contiguous operands stream as 16-byte
-// packs; broadcast operands are read through per-dimension strides (0 on a
-// broadcast dimension) of the output's multi-index, with no materialised
-// copy.
+// Broadcast element-wise combines of two or three operands, fp32 opmath
+// rounded once:
+//   BC_ADD          y = a + p * b            (torch.add; torch.sub passes -p, exact)
+//   BC_LERP_SCALAR  y = lerp(a, b, p)        (torch.lerp with a scalar weight)
+//   BC_LERP_TENSOR  y = lerp(a, b, w)        (torch.lerp with a weight tensor)
+// Same-shape contiguous operands stream as 16-byte packs; broadcast operands
+// are read through per-dimension strides (0 on a broadcast dimension) of the
+// output's multi-index, with no materialised copy.
 // ---------------------------------------------------------------------------
 constexpr int kMaxDims = 8;
+enum { BC_ADD = 0, BC_LERP_SCALAR = 1, BC_LERP_TENSOR = 2 };
 struct BcastDesc {
   int ndim;
   int64_t shape[kMaxDims];  // output shape
-  int64_t as[kMaxDims];     // element strides of a (0: broadcast)
-  int64_t bs[kMaxDims];     // element strides of b
+  int64_t st[3][kMaxDims];  // element strides of a, b, w (0: broadcast)
 };
 
-template <typename T>
-__global__ __launch_bounds__(256) void add_vec_kernel(const T* __restrict__ a,
-                                                      const T* __restrict__ b, T* __restrict__ y,
-                                                      int64_t npack, float alpha) {
+template <int OP> struct BcastArity { static constexpr int n = OP == BC_LERP_TENSOR ? 3 : 2; };
+
+// torch.lerp's two-sided form: start + w (end - start) for |w| < 0.5, else
+// end - (1 - w)(end - start), each as one fma: exact at w = 0 and w = 1.
+__device__ __forceinline__ float lerp_f32(float s, float e, float w) {
+  const float d = e - s;
+  return __builtin_fabsf(w) < 0.5f ? fmaf(w, d, s) : fmaf(w - 1.0f, d, e);
+}
+
+template <int OP>
+__device__ __forceinline__ float bc_apply(float a, float b, float w, float p) {
+  if constexpr (OP == BC_ADD) return fmaf(p, b, a);
+  else if constexpr (OP == BC_LERP_SCALAR) return lerp_f32(a, b, p);
+  else return lerp_f32(a, b, w);
+}
+
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void bcast_vec_kernel(const T* __restrict__ a,
+                                                        const T* __restrict__ b,
+                                                        const T* __restrict__ w,
+                                                        T* __restrict__ y, int64_t npack,
+                                                        float p) {
   constexpr int V = Elem<T>::kVec;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= npack) return;
   const Pack<T> pa = load_pack_nt(a + i * V), pb = load_pack_nt(b + i * V);
+  Pack<T> pw;
+  if constexpr (BcastArity<OP>::n == 3) pw = load_pack_nt(w + i * V);
   Pack<T> out;
 #pragma unroll
-  for (int e = 0; e < V; ++e)
-    out.v[e] = Elem<T>::from_f32(fmaf(alpha, Elem<T>::to_f32(pb.v[e]), Elem<T>::to_f32(pa.v[e])));
+  for (int e = 0; e < V; ++e) {
+    const float we = BcastArity<OP>::n == 3 ? Elem<T>::to_f32(pw.v[e]) : 0.0f;
+    out.v[e] = Elem<T>::from_f32(
+        bc_apply<OP>(Elem<T>::to_f32(pa.v[e]), Elem<T>::to_f32(pb.v[e]), we, p));
+  }
   store_pack_nt(y + i * V, out);
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void add_bcast_kernel(const T* __restrict__ a,
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void bcast_any_kernel(const T* __restrict__ a,
                                                         const T* __restrict__ b,
+                                                        const T* __restrict__ w,
                                                         T* __restrict__ y, int64_t begin,
-                                                        int64_t n, float alpha, BcastDesc d) {
+                                                        int64_t n, float p, BcastDesc d) {
+  constexpr int NOP = BcastArity<OP>::n;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    int64_t rem = i, ao = 0, bo = 0;
+    int64_t rem = i, off[3] = {0, 0, 0};
     for (int k = d.ndim - 1; k >= 0; --k) {
       const int64_t idx = rem % d.shape[k];
       rem /= d.shape[k];
-      ao += idx * d.as[k];
-      bo += idx * d.bs[k];
+#pragma unroll
+      for (int o = 0; o < NOP; ++o) off[o] += idx * d.st[o][k];
     }
-    y[i] = Elem<T>::from_f32(fmaf(alpha, Elem<T>::to_f32(b[bo]), Elem<T>::to_f32(a[ao])));
+    const float we = NOP == 3 ? Elem<T>::to_f32(w[off[2]]) : 0.0f;
+    y[i] = Elem<T>::from_f32(
+        bc_apply<OP>(Elem<T>::to_f32(a[off[0]]), Elem<T>::to_f32(b[off[1]]), we, p));
   }
 }
 
-// Broadcast operands whose innermost dimension is unit-stride or broadcast
-// (bias rows, per-channel scales): a thread takes one 16-byte pack of an output
-// row, so the outer multi-index is computed once per pack rather than per
-// element, in 32-bit arithmetic (I = uint32_t) when every offset fits.  A
-// broadcast operand (some stride 0) is re-read across rows and keeps the
-// cached load; a streamed one takes the non-temporal load.
-template <typename T, typename I>
-__global__ __launch_bounds__(256) void add_inner_kernel(const T* __restrict__ a,
-                                                        const T* __restrict__ b,
-                                                        T* __restrict__ y, I npack, I row_packs,
-                                                        float alpha, BcastDesc d, int a_bc,
-                                                        int b_bc) {
+// Operands whose innermost dimension is unit-stride or broadcast (bias rows,
+// per-channel scales): a thread takes one 16-byte pack of an output row, so
+// the outer multi-index is computed once per pack rather than per element,
+// in 32-bit arithmetic (I = uint32_t) when every offset fits.  A broadcast
+// operand (some stride 0) is re-read across rows and keeps the cached load;
+// a streamed one takes the non-temporal load.  Bit o of `vec_mask` marks
+// operand o as unit-stride along the row, bit o of `bc_mask` as broadcast
+// somewhere.
+template <typename T, int OP, typename I>
+__global__ __launch_bounds__(256) void bcast_inner_kernel(const T* __restrict__ a,
+                                                          const T* __restrict__ b,
+                                                          const T* __restrict__ w,
+                                                          T* __restrict__ y, I npack,
+                                                          I row_packs, float p, BcastDesc d,
+                                                          int vec_mask, int bc_mask) {
   constexpr int V = Elem<T>::kVec;
+  constexpr int NOP = BcastArity<OP>::n;
+  const T* src[3] = {a, b, w};
   const int nd = d.ndim;  // >= 1; dimension nd - 1 is the row
-  const bool a_vec = d.as[nd - 1] != 0, b_vec = d.bs[nd - 1] != 0;
   const I stride = (I)gridDim.x * blockDim.x;
-  for (I p = (I)blockIdx.x * blockDim.x + threadIdx.x; p < npack; p += stride) {
-    I r = p / row_packs;
-    const I c = (p - r * row_packs) * V;
-    I ao = a_vec ? c : 0, bo = b_vec ? c : 0;
+  for (I pk = (I)blockIdx.x * blockDim.x + threadIdx.x; pk < npack; pk += stride) {
+    I r = pk / row_packs;
+    const I c = (pk - r * row_packs) * V;
+    I off[3];
+#pragma unroll
+    for (int o = 0; o < NOP; ++o) off[o] = ((vec_mask >> o) & 1) ? c : 0;
     for (int k = nd - 2; k >= 0; --k) {
       const I sh = (I)d.shape[k], q = r / sh, idx = r - q * sh;
       r = q;
-      ao += idx * (I)d.as[k];
-      bo += idx * (I)d.bs[k];
-    }
-    Pack<T> pa, pb, out;
-    if (a_vec) {
-      pa = a_bc ? load_pack(a + ao) : load_pack_nt(a + ao);
-    } else {
-      const T v = a[ao];
 #pragma unroll
-      for (int e = 0; e < V; ++e) pa.v[e] = v;
+      for (int o = 0; o < NOP; ++o) off[o] += idx * (I)d.st[o][k];
     }
-    if (b_vec) {
-      pb = b_bc ? load_pack(b + bo) : load_pack_nt(b + bo);
-    } else {
-      const T v = b[bo];
+    Pack<T> in[3];
 #pragma unroll
-      for (int e = 0; e < V; ++e) pb.v[e] = v;
+    for (int o = 0; o < NOP; ++o) {
+      if ((vec_mask >> o) & 1) {
+        in[o] = ((bc_mask >> o) & 1) ? load_pack(src[o] + off[o]) : load_pack_nt(src[o] + off[o]);
+      } else {
+        const T v = src[o][off[o]];
+#pragma unroll
+        for (int e = 0; e < V; ++e) in[o].v[e] = v;
+      }
     }
+    Pack<T> out;
 #pragma unroll
-    for (int e = 0; e < V; ++e)
-      out.v[e] = Elem<T>::from_f32(fmaf(alpha, Elem<T>::to_f32(pb.v[e]), Elem<T>::to_f32(pa.v[e])));
-    store_pack_nt(y + (int64_t)p * V, out);
+    for (int e = 0; e < V; ++e) {
+      const float we = NOP == 3 ? Elem<T>::to_f32(in[2].v[e]) : 0.0f;
+      out.v[e] = Elem<T>::from_f32(
+          bc_apply<OP>(Elem<T>::to_f32(in[0].v[e]), Elem<T>::to_f32(in[1].v[e]), we, p));
+    }
+    store_pack_nt(y + (int64_t)pk * V, out);
   }
 }
 
 // Drops size-1 dimensions and merges a dimension into the one outside it
-// where both operands' strides chain (stride[k-1] == stride[k] * shape[k],
+// where every operand's strides chain (stride[k-1] == stride[k] * shape[k],
 // broadcast dimensions included), so the index arithmetic runs over as few
 // dimensions as the layout allows.
-static void coalesce_dims(BcastDesc& d) {
+static void coalesce_dims(BcastDesc& d, int nop) {
   BcastDesc o{};
   int m = 0;
   for (int k = 0; k < d.ndim; ++k) {
     if (d.shape[k] == 1) continue;
-    if (m > 0 && o.as[m - 1] == d.as[k] * d.shape[k] && o.bs[m - 1] == d.bs[k] * d.shape[k]) {
+    bool chain = m > 0;
+    for (int q = 0; q < nop && chain; ++q) chain = o.st[q][m - 1] == d.st[q][k] * d.shape[k];
+    if (chain) {
       o.shape[m - 1] *= d.shape[k];
-      o.as[m - 1] = d.as[k];
-      o.bs[m - 1] = d.bs[k];
+      for (int q = 0; q < nop; ++q) o.st[q][m - 1] = d.st[q][k];
     } else {
       o.shape[m] = d.shape[k];
-      o.as[m] = d.as[k];
-      o.bs[m] = d.bs[k];
+      for (int q = 0; q < nop; ++q) o.st[q][m] = d.st[q][k];
       ++m;
     }
   }
@@ -521,64 +557,106 @@ static void coalesce_dims(BcastDesc& d) {
 // The pack kernel applies when the row length is a whole number of packs,
 // each operand's row is unit-stride (16-byte aligned base and row offsets) or
 // broadcast, and the output is 16-byte aligned.  Returns false otherwise.
-template <typename T>
-static bool launch_add_inner(const T* a, const T* b, T* y, const BcastDesc& d, int64_t n,
-                             float alpha, hipStream_t s) {
+template <typename T, int OP>
+static bool launch_bcast_inner(const T* const (&src)[3], T* y, const BcastDesc& d, int64_t n,
+                               float p, hipStream_t s) {
   constexpr int V = Elem<T>::kVec;
+  constexpr int NOP = BcastArity<OP>::n;
   const int nd = d.ndim;
   if (nd < 1 || d.shape[nd - 1] % V != 0 || !host_aligned16(y)) return false;
-  int64_t amax = 0, bmax = 0;
-  bool a_bc = false, b_bc = false;
-  for (int k = 0; k < nd; ++k) {
-    amax += (d.shape[k] - 1) * d.as[k];
-    bmax += (d.shape[k] - 1) * d.bs[k];
-    a_bc |= d.as[k] == 0;
-    b_bc |= d.bs[k] == 0;
+  int vec_mask = 0, bc_mask = 0;
+  bool fits32 = true;
+  for (int o = 0; o < NOP; ++o) {
+    int64_t omax = 0;
+    for (int k = 0; k < nd; ++k) {
+      omax += (d.shape[k] - 1) * d.st[o][k];
+      if (d.st[o][k] == 0) bc_mask |= 1 << o;
+    }
+    fits32 &= omax < (int64_t)UINT32_MAX;
+    const int64_t in = d.st[o][nd - 1];
+    if (in != 0 && in != 1) return false;
+    if (in == 1) {
+      vec_mask |= 1 << o;
+      if (!host_aligned16(src[o])) return false;
+      for (int k = 0; k < nd - 1; ++k)
+        if (d.st[o][k] % V) return false;
+    }
   }
-  const int64_t ain = d.as[nd - 1], bin = d.bs[nd - 1];
-  if ((ain != 0 && ain != 1) || (bin != 0 && bin != 1)) return false;
-  for (int k = 0; k < nd - 1; ++k)
-    if ((ain && d.as[k] % V) || (bin && d.bs[k] % V)) return false;
-  if ((ain && !host_aligned16(a)) || (bin && !host_aligned16(b))) return false;
   const int64_t npack = n / V, row_packs = d.shape[nd - 1] / V;
   const unsigned grid = (unsigned)stream_grid(npack, 256);
-  if (npack < (int64_t)UINT32_MAX - (int64_t)grid * 256 && amax < (int64_t)UINT32_MAX &&
-      bmax < (int64_t)UINT32_MAX)
-    add_inner_kernel<T, uint32_t><<<dim3(grid), dim3(256), 0, s>>>(
-        a, b, y, (uint32_t)npack, (uint32_t)row_packs, alpha, d, a_bc, b_bc);
+  if (fits32 && npack < (int64_t)UINT32_MAX - (int64_t)grid * 256)
+    bcast_inner_kernel<T, OP, uint32_t><<<dim3(grid), dim3(256), 0, s>>>(
+        src[0], src[1], src[2], y, (uint32_t)npack, (uint32_t)row_packs, p, d, vec_mask, bc_mask);
   else
-    add_inner_kernel<T, int64_t><<<dim3(grid), dim3(256), 0, s>>>(a, b, y, npack, row_packs,
-                                                                   alpha, d, a_bc, b_bc);
+    bcast_inner_kernel<T, OP, int64_t><<<dim3(grid), dim3(256), 0, s>>>(
+        src[0], src[1], src[2], y, npack, row_packs, p, d, vec_mask, bc_mask);
   return true;
 }
 
-template <typename T>
-static int launch_add(const void* av, const void* bv, void* yv, BcastDesc d, int64_t n,
-                      float alpha, hipStream_t s) {
-  const T* a = static_cast<const T*>(av);
-  const T* b = static_cast<const T*>(bv);
-  T* y = static_cast<T*>(yv);
+template <typename T, int OP>
+static int launch_bcast(const void* av, const void* bv, const void* wv, void* yv, BcastDesc d,
+                        int64_t n, float p, hipStream_t s) {
   constexpr int V = Elem<T>::kVec;
-  coalesce_dims(d);
-  bool flat = true;  // both operands contiguous over the whole output
-  int64_t expect = 1;
-  for (int k = d.ndim - 1; k >= 0; --k) {
-    if (d.shape[k] != 1 && (d.as[k] != expect || d.bs[k] != expect)) flat = false;
-    expect *= d.shape[k];
+  constexpr int NOP = BcastArity<OP>::n;
+  const T* const src[3] = {static_cast<const T*>(av), static_cast<const T*>(bv),
+                           static_cast<const T*>(wv)};
+  T* y = static_cast<T*>(yv);
+  coalesce_dims(d, NOP);
+  bool flat = true;  // every operand contiguous over the whole output
+  bool aligned = host_aligned16(y);
+  for (int o = 0; o < NOP; ++o) {
+    int64_t expect = 1;
+    for (int k = d.ndim - 1; k >= 0; --k) {
+      if (d.shape[k] != 1 && d.st[o][k] != expect) flat = false;
+      expect *= d.shape[k];
+    }
+    aligned &= host_aligned16(src[o]);
   }
+  if (!flat && launch_bcast_inner<T, OP>(src, y, d, n, p, s)) return launch_status();
   int64_t npack = 0;
-  if (!flat && launch_add_inner<T>(a, b, y, d, n, alpha, s)) return launch_status();
-  if (flat && host_aligned16(a) && host_aligned16(b) && host_aligned16(y)) {
+  if (flat && aligned) {
     npack = n / V;
     if (npack > 0)
-      add_vec_kernel<T><<<dim3((unsigned)((npack + 255) / 256)), dim3(256), 0, s>>>(a, b, y, npack,
-                                                                                  alpha);
+      bcast_vec_kernel<T, OP><<<dim3((unsigned)((npack + 255) / 256)), dim3(256), 0, s>>>(
+          src[0], src[1], src[2], y, npack, p);
   }
   const int64_t done = npack * V;
   if (done < n)
-    add_bcast_kernel<T><<<dim3((unsigned)stream_grid(n - done, 256)), dim3(256), 0, s>>>(
-        a, b, y, done, n, alpha, d);
+    bcast_any_kernel<T, OP><<<dim3((unsigned)stream_grid(n - done, 256)), dim3(256), 0, s>>>(
+        src[0], src[1], src[2], y, done, n, p, d);
   return launch_status();
+}
+
+// Shared argument checks of the broadcast entry points; fills `d` and `n`.
+static int bcast_prepare(int ndim, const int64_t* out_shape, const int64_t* const (&strides)[3],
+                         int nop, BcastDesc& d, int64_t& n) {
+  if (ndim < 0 || ndim > kMaxDims) return TILEOPS_ESHAPE;
+  if (ndim > 0 && !out_shape) return TILEOPS_ENULL;
+  for (int o = 0; o < nop; ++o)
+    if (ndim > 0 && !strides[o]) return TILEOPS_ENULL;
+  d = BcastDesc{};
+  d.ndim = ndim;
+  n = 1;
+  for (int k = 0; k < ndim; ++k) {
+    if (out_shape[k] < 0) return TILEOPS_ESHAPE;
+    d.shape[k] = out_shape[k];
+    for (int o = 0; o < nop; ++o) {
+      if (strides[o][k] < 0) return TILEOPS_EINVAL;
+      d.st[o][k] = strides[o][k];
+    }
+    n *= out_shape[k];
+  }
+  return 0;
+}
+
+template <int OP>
+static int dispatch_bcast(int dtype, const void* a, const void* b, const void* w, void* y,
+                          const BcastDesc& d, int64_t n, float p, hipStream_t s) {
+  switch (dtype) {
+    case TILEOPS_F32: return launch_bcast<float, OP>(a, b, w, y, d, n, p, s);
+    case TILEOPS_F16: return launch_bcast<f16, OP>(a, b, w, y, d, n, p, s);
+    default: return launch_bcast<bf16, OP>(a, b, w, y, d, n, p, s);
+  }
 }
 
 }  // namespace tileops
@@ -586,28 +664,31 @@ static int launch_add(const void* av, const void* bv, void* yv, BcastDesc d, int
 extern "C" int tileops_add_fwd(const void* a, const void* b, void* y, int ndim,
                                const int64_t* out_shape, const int64_t* a_strides,
                                const int64_t* b_strides, float alpha, int dtype, void* stream) {
-  if (ndim < 0 || ndim > kMaxDims) return TILEOPS_ESHAPE;
-  if (ndim > 0 && (!out_shape || !a_strides || !b_strides)) return TILEOPS_ENULL;
-  BcastDesc d{};
-  d.ndim = ndim;
-  int64_t n = 1;
-  for (int k = 0; k < ndim; ++k) {
-    if (out_shape[k] < 0) return TILEOPS_ESHAPE;
-    if (a_strides[k] < 0 || b_strides[k] < 0) return TILEOPS_EINVAL;
-    d.shape[k] = out_shape[k];
-    d.as[k] = a_strides[k];
-    d.bs[k] = b_strides[k];
-    n *= out_shape[k];
-  }
+  BcastDesc d;
+  int64_t n = 0;
+  const int64_t* const st[3] = {a_strides, b_strides, nullptr};
+  if (int e = bcast_prepare(ndim, out_shape, st, 2, d, n)) return e;
+  if (dtype < TILEOPS_F32 || dtype > TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (n == 0) return 0;
+  if (!a || !b || !y) return TILEOPS_ENULL;
+  return dispatch_bcast<BC_ADD>(dtype, a, b, nullptr, y, d, n, alpha,
+                                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tileops_lerp_fwd(const void* a, const void* b, const void* w, void* y, int ndim,
+                                const int64_t* out_shape, const int64_t* a_strides,
+                                const int64_t* b_strides, const int64_t* w_strides, float weight,
+                                int dtype, void* stream) {
+  BcastDesc d;
+  int64_t n = 0;
+  const int64_t* const st[3] = {a_strides, b_strides, w_strides};
+  if (int e = bcast_prepare(ndim, out_shape, st, w ? 3 : 2, d, n)) return e;
   if (dtype < TILEOPS_F32 || dtype > TILEOPS_BF16) return TILEOPS_EINVAL;
   if (n == 0) return 0;
   if (!a || !b || !y) return TILEOPS_ENULL;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case TILEOPS_F32: return launch_add<float>(a, b, y, d, n, alpha, s);
-    case TILEOPS_F16: return launch_add<f16>(a, b, y, d, n, alpha, s);
-    default: return launch_add<bf16>(a, b, y, d, n, alpha, s);
-  }
+  if (w) return dispatch_bcast<BC_LERP_TENSOR>(dtype, a, b, w, y, d, n, 0.0f, s);
+  return dispatch_bcast<BC_LERP_SCALAR>(dtype, a, b, nullptr, y, d, n, weight, s);
 }
 
 extern "C" int tileops_bitwise_not_fwd(const void* x, void* y, int64_t nbytes, int is_bool,

@@ -79,6 +79,10 @@ SIGNATURES = {
     ),
     "tileops_bitwise_not_fwd": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
     "tileops_add_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_float, _c_int, _c_p]),
+    "tileops_lerp_fwd": (
+        _c_int,
+        [_c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p, _c_float, _c_int, _c_p],
+    ),
     "tileops_gla_decode_fwd": (
         _c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float,

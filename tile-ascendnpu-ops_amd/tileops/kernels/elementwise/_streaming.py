@@ -34,10 +34,9 @@ def _check_dtype(cls: type, dtype: torch.dtype, supported: tuple) -> None:
 class UnaryFwdKernel(Kernel):
     """y = f(x) over a flat vector of ``N_total`` elements (fp32 opmath)."""
 
-    supported_archs: Optional[list] = None
     SUPPORTED_DTYPES = _FLOAT_DTYPES
     _unary_op: int = -1
-    profile_kernel_name = "unary_vec_kernel"
+    profile_kernel_name = r"tileops\d+unary_(vec|scalar)_kernel"
 
     def __init__(self, N_total: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()
@@ -49,18 +48,27 @@ class UnaryFwdKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # 16-byte packs per lane, 4 packs in flight per thread (compiled in)
-        return {"vector_bytes": 16, "unroll": 4}
+        # unary_vec_kernel: 256-thread workgroups, one 16-byte non-temporal
+        # pack per thread, a grid covering the whole tensor
+        return {"threads": 256, "vector_bytes": 16, "packs_per_thread": 1}
 
     def _bounds(self) -> tuple[float, float, int]:
         return 0.0, 0.0, 0
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``out`` (contiguous, same dtype and size) receives the result; it
+        may be ``x`` itself: every element is read before it is written by
+        the same thread, so the kernel runs in place."""
         _native.require_device(x)
+        self.check_tensor("x", x, dtype=self.dtype, numel=self.N_total)
         x = x.contiguous()
-        if x.numel() != self.N_total:
-            raise ValueError(f"Expected {self.N_total} elements, got {x.numel()}")
-        y = torch.empty_like(x)
+        if out is None:
+            y = torch.empty_like(x)
+        else:
+            self.check_tensor("out", out, dtype=self.dtype, numel=self.N_total)
+            if not out.is_contiguous():
+                raise ValueError(f"{type(self).__name__}: out must be contiguous")
+            y = out
         lo, hi, flags = self._bounds()
         code = _native.lib().tileops_unary_fwd(
             self._unary_op,
@@ -80,10 +88,9 @@ class UnaryFwdKernel(Kernel):
 class PredicateFwdKernel(Kernel):
     """y = pred(x) as torch.bool over a flat vector of ``N_total`` elements."""
 
-    supported_archs: Optional[list] = None
     SUPPORTED_DTYPES = _FLOAT_DTYPES
     _predicate: int = -1
-    profile_kernel_name = "isfp_vec_kernel"
+    profile_kernel_name = r"tileops\d+isfp_(vec|scalar)_kernel"
 
     def __init__(self, N_total: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()
@@ -95,14 +102,14 @@ class PredicateFwdKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # 16 predicates per lane -> one 16-byte bool store
-        return {"elements_per_lane": 16, "unroll": 2}
+        # isfp_vec_kernel: 256-thread workgroups, two 16-byte input packs per
+        # thread (256 packs apart), each giving a 4- or 8-byte bool store
+        return {"threads": 256, "vector_bytes": 16, "packs_per_thread": 2}
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         _native.require_device(x)
+        self.check_tensor("x", x, dtype=self.dtype, numel=self.N_total)
         x = x.contiguous()
-        if x.numel() != self.N_total:
-            raise ValueError(f"Expected {self.N_total} elements, got {x.numel()}")
         y = torch.empty(x.shape, dtype=torch.bool, device=x.device)
         code = _native.lib().tileops_isfp_fwd(
             self._predicate,
@@ -119,10 +126,9 @@ class PredicateFwdKernel(Kernel):
 class GatedGeluFwdKernel(Kernel):
     """y[M, N] = gelu(x[:, :N]) * x[:, N:] for x[M, 2N] (fp32 opmath)."""
 
-    supported_archs: Optional[list] = None
     SUPPORTED_DTYPES = _FLOAT_DTYPES
     _approx: int = 0
-    profile_kernel_name = "gated_gelu_vec_kernel"
+    profile_kernel_name = r"tileops\d+gated_gelu_(vec|scalar)_kernel"
 
     def __init__(self, M: int, N: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()
@@ -135,14 +141,14 @@ class GatedGeluFwdKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # one workgroup row per output row, 2 packs of gate and value in flight
-        return {"threads": 256, "unroll": 2}
+        # gated_gelu_vec_kernel: grid (column blocks, rows), 256-thread
+        # workgroups, two 16-byte gate packs and two value packs per thread
+        return {"threads": 256, "vector_bytes": 16, "packs_per_thread": 2}
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         _native.require_device(x)
+        self.check_tensor("x", x, dtype=self.dtype, shape=(self.M, 2 * self.N))
         x = x.contiguous()
-        if tuple(x.shape) != (self.M, 2 * self.N):
-            raise ValueError(f"Expected x.shape {(self.M, 2 * self.N)}, got {tuple(x.shape)}")
         y = torch.empty((self.M, self.N), dtype=self.dtype, device=x.device)
         code = _native.lib().tileops_gated_gelu_fwd(
             self._approx,

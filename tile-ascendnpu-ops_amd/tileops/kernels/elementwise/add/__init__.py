@@ -1,3 +1,3 @@
-from tileops.kernels.elementwise.add.add import AddFwdKernel, SubFwdKernel
+from tileops.kernels.elementwise.add.add import AddFwdKernel
 
-__all__ = ["AddFwdKernel", "SubFwdKernel"]
+__all__ = ["AddFwdKernel"]

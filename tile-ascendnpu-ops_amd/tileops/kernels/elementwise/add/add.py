@@ -1,12 +1,12 @@
-"""AddFwdKernel / SubFwdKernel: y = a +- alpha * b with broadcasting on gfx950.
+"""AddFwdKernel: y = a + alpha * b with broadcasting on gfx950.
 
-Reference classes: examples/TileOPs/tileops/kernels/elementwise/add, sub
-(``(N_total, dtype, alpha, config=None)``; torch.add / torch.sub with fp32
-opmath).  The reference Ops materialised the broadcast with
-``expand().contiguous()`` and ran a flat kernel; here the kernel reads each
-operand through per-dimension strides (0 on a broadcast dimension), so no
-copy is made.  Device code: add_vec_kernel / add_bcast_kernel in
-csrc/elementwise.hip (subtraction passes -alpha, which is exact).
+Reference class: examples/TileOPs/tileops/kernels/elementwise/add
+(``(N_total, dtype, alpha, config=None)``; torch.add with fp32 opmath).  The
+reference Ops materialised the broadcast with ``expand().contiguous()`` and
+ran a flat kernel; here the kernel reads each operand through per-dimension
+strides (0 on a broadcast dimension), so no copy is made.  Device code:
+bcast_vec_kernel / bcast_inner_kernel / bcast_any_kernel with BC_ADD in
+csrc/elementwise.hip.
 """
 
 import ctypes
@@ -17,9 +17,9 @@ import torch
 from tileops import _native
 from tileops.kernels.kernel_base import Kernel
 
-__all__ = ["AddFwdKernel", "SubFwdKernel", "broadcast_strides"]
+__all__ = ["AddFwdKernel", "BroadcastFwdKernel", "broadcast_strides", "MAX_DIMS"]
 
-_MAX_DIMS = 8
+MAX_DIMS = 8
 
 
 def broadcast_strides(t: torch.Tensor, out_shape: Sequence[int]) -> list:
@@ -33,7 +33,51 @@ def broadcast_strides(t: torch.Tensor, out_shape: Sequence[int]) -> list:
     return strides
 
 
-class AddFwdKernel(Kernel):
+class BroadcastFwdKernel(Kernel):
+    """Shared flow of the broadcasting element-wise kernels: validate the
+    operands, form the broadcast output shape and each operand's strides,
+    and hand them to the C ABI as host arrays."""
+
+    SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+    profile_kernel_name = r"tileops\d+bcast_(vec|inner|any)_kernel"
+
+    def _init_common(self, N_total: int, dtype: torch.dtype, config: Optional[dict]) -> None:
+        if dtype not in self.SUPPORTED_DTYPES:
+            names = ", ".join(str(dt) for dt in self.SUPPORTED_DTYPES)
+            raise ValueError(f"{type(self).__name__} only supports dtypes [{names}], got {dtype}")
+        self.N_total = int(N_total)
+        self.dtype = dtype
+        self.output_dtype = dtype
+        self.init_config(config)
+
+    @property
+    def default_config(self) -> dict:
+        # bcast_vec_kernel / bcast_inner_kernel: 256-thread workgroups, one
+        # 16-byte pack per thread; operands of up to 8 broadcast dimensions
+        return {"threads": 256, "vector_bytes": 16, "max_dims": MAX_DIMS}
+
+    def _operands(self, names: Sequence[str], tensors: Sequence[torch.Tensor]):
+        """``(out_shape, y, ndim, shape_arr, [stride_arr, ...])`` for the operands."""
+        _native.require_device(*tensors)
+        for name, t in zip(names, tensors):
+            self.check_tensor(name, t, dtype=self.dtype)
+        out_shape = tuple(torch.broadcast_shapes(*(t.shape for t in tensors)))
+        if len(out_shape) > MAX_DIMS:
+            raise ValueError(f"{type(self).__name__} supports at most {MAX_DIMS} dims")
+        n = 1
+        for d in out_shape:
+            n *= d
+        if n != self.N_total:
+            raise ValueError(f"{type(self).__name__}: expected {self.N_total} output elements, "
+                             f"got {n}")
+        y = torch.empty(out_shape, dtype=self.dtype, device=tensors[0].device)
+        nd = len(out_shape)
+        arr = ctypes.c_int64 * max(nd, 1)
+        strides = [arr(*broadcast_strides(t, out_shape)) for t in tensors]
+        return out_shape, y, nd, arr(*out_shape), strides
+
+
+class AddFwdKernel(BroadcastFwdKernel):
     """y = a + alpha * b over the broadcast shape of the operands.
 
     Args:
@@ -43,49 +87,17 @@ class AddFwdKernel(Kernel):
         config: Optional config override.
     """
 
-    supported_archs: Optional[list] = None
-    SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
-    profile_kernel_name = "add_"
     _sign = 1.0
 
     def __init__(self, N_total: int, dtype: torch.dtype, alpha=1, config: Optional[dict] = None):
         super().__init__()
-        if dtype not in self.SUPPORTED_DTYPES:
-            names = ", ".join(str(dt) for dt in self.SUPPORTED_DTYPES)
-            raise ValueError(f"{type(self).__name__} only supports dtypes [{names}], got {dtype}")
-        self.N_total = int(N_total)
-        self.dtype = dtype
         self.alpha = alpha
-        self.init_config(config)
-
-    @property
-    def default_config(self) -> dict:
-        return {"vector_bytes": 16, "max_dims": _MAX_DIMS}
+        self._init_common(N_total, dtype, config)
 
     def forward(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-        _native.require_device(a, b)
-        out_shape = tuple(torch.broadcast_shapes(a.shape, b.shape))
-        if len(out_shape) > _MAX_DIMS:
-            raise ValueError(f"{type(self).__name__} supports at most {_MAX_DIMS} dims")
-        n = 1
-        for d in out_shape:
-            n *= d
-        if n != self.N_total:
-            raise ValueError(f"Expected {self.N_total} output elements, got {n}")
-        y = torch.empty(out_shape, dtype=self.dtype, device=a.device)
-        nd = len(out_shape)
-        shape = (ctypes.c_int64 * max(nd, 1))(*out_shape)
-        sa = (ctypes.c_int64 * max(nd, 1))(*broadcast_strides(a, out_shape))
-        sb = (ctypes.c_int64 * max(nd, 1))(*broadcast_strides(b, out_shape))
+        _shape, y, nd, shape, (sa, sb) = self._operands(("a", "b"), (a, b))
         code = _native.lib().tileops_add_fwd(
             a.data_ptr(), b.data_ptr(), y.data_ptr(), nd, shape, sa, sb,
             float(self._sign * self.alpha), _native.dtype_code(self.dtype), _native.stream_of(a))
         _native.check(code, type(self).__name__)
         return y
-
-
-class SubFwdKernel(AddFwdKernel):
-    """y = a - alpha * b (``torch.sub``): the add kernel with -alpha."""
-
-    _sign = -1.0
-

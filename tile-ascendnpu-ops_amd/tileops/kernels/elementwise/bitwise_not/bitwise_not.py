@@ -28,9 +28,8 @@ class BitwiseNotFwdKernel(Kernel):
         config: Optional config override.
     """
 
-    supported_archs: Optional[list] = None
     SUPPORTED_DTYPES = BITWISE_DTYPES
-    profile_kernel_name = "bitnot_vec_kernel"
+    profile_kernel_name = r"tileops\d+bitnot_(vec|byte)_kernel"
 
     def __init__(self, N_total: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()
@@ -44,15 +43,13 @@ class BitwiseNotFwdKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        return {"vector_bytes": 16}
+        # bitnot_vec_kernel: 256-thread workgroups, one 16-byte pack per thread
+        return {"threads": 256, "vector_bytes": 16}
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         _native.require_device(x)
+        self.check_tensor("x", x, dtype=self.dtype, numel=self.N_total)
         x = x.contiguous()
-        if x.numel() != self.N_total:
-            raise ValueError(f"Expected {self.N_total} elements, got {x.numel()}")
-        if x.dtype != self.dtype:
-            raise ValueError(f"Expected dtype {self.dtype}, got {x.dtype}")
         y = torch.empty_like(x)
         code = _native.lib().tileops_bitwise_not_fwd(
             x.data_ptr(), y.data_ptr(), self.N_total * x.element_size(),

@@ -1,4 +1,4 @@
-from tileops.ops.elementwise.add import AddFwdOp, SubFwdOp
+from tileops.ops.elementwise.add import AddFwdOp
 from tileops.ops.elementwise.bitwise_not import BitwiseNotFwdOp
 from tileops.ops.elementwise.clamp_min import ClampMinFwdOp
 from tileops.ops.elementwise.clamp_scalar import ClampScalarFwdOp
@@ -9,7 +9,10 @@ from tileops.ops.elementwise.hardswish import HardswishFwdOp
 from tileops.ops.elementwise.isfinite import IsfiniteFwdOp
 from tileops.ops.elementwise.isinf import IsinfFwdOp
 from tileops.ops.elementwise.isnan import IsnanFwdOp
+from tileops.ops.elementwise.lerp_scalar import LerpFwdOp
+from tileops.ops.elementwise.lerp_tensor import LerpTensorFwdOp
 from tileops.ops.elementwise.mish import MishFwdOp
+from tileops.ops.elementwise.sub import SubFwdOp
 
 __all__ = [
     "AddFwdOp",
@@ -24,5 +27,7 @@ __all__ = [
     "IsfiniteFwdOp",
     "IsinfFwdOp",
     "IsnanFwdOp",
+    "LerpFwdOp",
+    "LerpTensorFwdOp",
     "MishFwdOp",
 ]

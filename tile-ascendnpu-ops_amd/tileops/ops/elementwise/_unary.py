@@ -78,6 +78,12 @@ class InplaceActivationOp(FlatElementwiseOp):
     def forward(self, input: torch.Tensor) -> torch.Tensor:
         self._validate_input(input)
         if self.inplace:
+            if input.is_contiguous():
+                # the kernel writes each element over the one it read: no
+                # second buffer and no copy back
+                flat = input.reshape(-1)
+                self.kernel(flat, out=flat)
+                return input
             result = self._eager_forward(input)
             input.copy_(result.reshape(input.shape))
             return input

@@ -1,7 +1,7 @@
-"""AddFwdOp / SubFwdOp: y = input +- alpha * other with PyTorch broadcasting.
+"""AddFwdOp: y = input + alpha * other with PyTorch broadcasting.
 
-Reference: examples/TileOPs/tileops/ops/elementwise/add.py:61-155 and
-sub.py (constructor ``(*, input: shape, other: shape, dtype, alpha=1)``,
+Reference: examples/TileOPs/tileops/ops/elementwise/add.py:61-155
+(constructor ``(*, input: shape, other: shape, dtype, alpha=1)``,
 float dtypes, the rejection message "AddFwdOp does not support dtype ...",
 ``out_shape = broadcast_shapes(input, other)``; roofline flops
 ``(1 if alpha == 1 else 2) * N``, bytes ``3 * N * elem_bytes`` with N the
@@ -14,11 +14,11 @@ from typing import Dict, Optional
 import torch
 
 from tileops.device import get_device_backend
-from tileops.kernels.elementwise.add import AddFwdKernel, SubFwdKernel
+from tileops.kernels.elementwise.add import AddFwdKernel
 from tileops.kernels.kernel_base import Kernel
 from tileops.ops.op_base import Op
 
-__all__ = ["AddFwdOp", "SubFwdOp"]
+__all__ = ["AddFwdOp"]
 
 
 class AddFwdOp(Op):
@@ -74,9 +74,3 @@ class AddFwdOp(Op):
         flops = (1 if self.alpha == 1 else 2) * n_total
         return flops, 3 * n_total * self.dtype.itemsize
 
-
-class SubFwdOp(AddFwdOp):
-    """Element-wise ``y = input - alpha * other`` with broadcasting."""
-
-    _op_name = "sub"
-    kernel_cls = SubFwdKernel

@@ -16,7 +16,7 @@ class HardswishFwdOp(InplaceActivationOp):
     Args:
         N_total: Total number of elements (flattened input).
         dtype: float16, bfloat16 or float32.
-        inplace: Copy the result into ``input`` and return ``input``.
+        inplace: Write the result into ``input`` and return ``input``.
         kernel_map: Optional kernel dispatch override.
     """
 

@@ -48,6 +48,49 @@ class BinaryWorkload(WorkloadBase):
                 torch.randn(self.other_shape, device=dev).to(self.dtype))
 
 
+class AddWorkload(BinaryWorkload):
+    """Operands of AddFwdOp (reference name: workloads/elementwise.py AddWorkload)."""
+
+
+class SubWorkload(BinaryWorkload):
+    """Operands of SubFwdOp (reference name: workloads/elementwise.py SubWorkload)."""
+
+
+class LerpScalarWorkload(WorkloadBase):
+    """Operands of LerpFwdOp: randn ``input`` and ``end`` of their own shapes
+    (broadcast together by the op; the weight is an op parameter)."""
+
+    def __init__(self, input_shape: tuple, end_shape: tuple, dtype: torch.dtype):
+        self.input_shape = tuple(input_shape)
+        self.end_shape = tuple(end_shape)
+        self.shape = self.input_shape
+        self.out_shape = tuple(torch.broadcast_shapes(self.input_shape, self.end_shape))
+        self.n_total = prod(self.out_shape) if self.out_shape else 1
+        self.dtype = dtype
+
+    def gen_inputs(self):
+        dev = get_device_backend().name
+        return (torch.randn(self.input_shape, device=dev).to(self.dtype),
+                torch.randn(self.end_shape, device=dev).to(self.dtype))
+
+
+class LerpTensorManifestWorkload(WorkloadBase):
+    """Operands of LerpTensorFwdOp at one manifest shape: randn ``input`` and
+    ``end``, ``weight`` uniform on [0, 1) (interpolation weights)."""
+
+    def __init__(self, shape: tuple, dtype: torch.dtype):
+        self.shape = tuple(shape)
+        self.input_shape = self.end_shape = self.weight_shape = self.shape
+        self.n_total = prod(self.shape)
+        self.dtype = dtype
+
+    def gen_inputs(self):
+        dev = get_device_backend().name
+        return (torch.randn(self.shape, device=dev).to(self.dtype),
+                torch.randn(self.shape, device=dev).to(self.dtype),
+                torch.rand(self.shape, device=dev).to(self.dtype))
+
+
 class BitwiseNotWorkload(WorkloadBase):
     """Input of BitwiseNotFwdOp: random bits of the dtype (bool: 0 / 1)."""
 
