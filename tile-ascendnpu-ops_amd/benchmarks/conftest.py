@@ -21,6 +21,18 @@ from tileops.benchmark.benchmark_base import BenchmarkReport, _bench_results  # 
 from tileops.device import get_device_backend  # noqa: E402
 
 
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an AMD GPU (launches HIP kernels)")
+
+
+def pytest_collection_modifyitems(config, items):
+    # every benchmark case launches HIP kernels: `-m "not gpu"` deselects them
+    here = os.path.dirname(os.path.abspath(__file__))
+    for item in items:
+        if str(item.fspath).startswith(here):
+            item.add_marker(pytest.mark.gpu)
+
+
 def pytest_collect_file(file_path, parent):
     # files named on the command line are collected by pytest itself
     if (file_path.suffix == ".py" and file_path.name.startswith("bench_")

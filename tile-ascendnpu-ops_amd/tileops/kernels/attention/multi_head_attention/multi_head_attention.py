@@ -67,9 +67,8 @@ class GQAPrefillFwdKernel(Kernel):
         config: Optional config override.
     """
 
-    supported_archs: Optional[list] = None
     SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
-    profile_kernel_name = "mha_fwd_kernel"
+    profile_kernel_name = r"mha\d+mha_fwd_kernel"
 
     def __init__(
         self,
@@ -113,8 +112,9 @@ class GQAPrefillFwdKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # query rows per workgroup, key rows per LDS tile (compiled in)
-        return {"block_m": 128, "block_n": 64, "num_stages": 1}
+        # mha_fwd_kernel: 256 query rows per 512-thread workgroup (8
+        # wavefronts x 32 rows), 64-key K / V tiles in three LDS slots
+        return {"block_m": 256, "block_n": 64, "num_stages": 3, "threads": 512}
 
     def forward(
         self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor

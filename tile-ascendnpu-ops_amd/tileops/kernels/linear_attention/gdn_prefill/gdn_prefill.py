@@ -33,9 +33,8 @@ class GDNPrefillFwdKernel(Kernel):
         config: Optional config override.
     """
 
-    supported_archs: Optional[list] = None
     SUPPORTED_DTYPES = (torch.bfloat16,)
-    profile_kernel_name = "gdn_recur_kernel"
+    profile_kernel_name = r"gdn\d+gdn_(prep|recur)_kernel"
 
     def __init__(
         self,

@@ -48,12 +48,13 @@ class GLADecodeKernel(Kernel):
         B, H, DK, DV: batch / heads / key dim / value dim.
         dtype: float16, bfloat16 or float32.
         scale: readout scale; non-positive means ``DK ** -0.5``.
-        k_tile: accepted for interface parity (unused).
+        k_tile: accepted for interface parity; the kernel streams the whole
+            state in one pass, so it selects nothing.
         config: Optional config override.
     """
 
-    supported_archs: Optional[list] = None
     SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+    profile_kernel_name = r"gla\d+gla_decode_kernel"
 
     def __init__(
         self,
@@ -85,7 +86,8 @@ class GLADecodeKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        return {"k_tile": self.k_tile}
+        # gla_decode_kernel: one 256-thread workgroup per (batch, head)
+        return {"threads": 256}
 
     def forward(
         self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gk: torch.Tensor,

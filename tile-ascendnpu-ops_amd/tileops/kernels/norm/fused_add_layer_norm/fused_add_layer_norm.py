@@ -10,7 +10,8 @@ Per row of N elements::
 with mean / biased variance of the rounded sum in fp32.  ``forward`` returns a
 list ``[y, residual_out]`` shaped like ``x``.  ``weight`` / ``bias`` may be the
 input dtype (the reference contract) or float32.
-Device code: fused_add_ln_reg_kernel in csrc/norm.hip.
+Device code: fused_add_ln_wave_kernel (N a multiple of 8 up to 8192) and
+fused_add_ln_generic_kernel in csrc/norm.hip.
 """
 
 from typing import Optional
@@ -34,9 +35,8 @@ class FusedAddLayerNormKernel(Kernel):
         config: Optional config override.
     """
 
-    supported_archs: Optional[list] = None
     SUPPORTED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
-    profile_kernel_name = "fused_add_ln"
+    profile_kernel_name = r"tileops\d+fused_add_ln_(wave|generic)_kernel"
 
     def __init__(
         self,
@@ -60,7 +60,9 @@ class FusedAddLayerNormKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # one wavefront per row, row held in registers, w/b staged in LDS
+        # fused_add_ln_wave_kernel: one wavefront per row with the row held in
+        # registers, four rows per 256-thread workgroup, weight / bias staged
+        # in LDS as fp32
         return {"rows_per_wave": 1, "rows_per_workgroup": 4}
 
     def forward(
@@ -71,6 +73,13 @@ class FusedAddLayerNormKernel(Kernel):
         bias: torch.Tensor,
     ) -> list[torch.Tensor]:
         _native.require_device(x, residual, weight, bias)
+        self.check_tensor("x", x, dtype=self.dtype, numel=self.M * self.N)
+        if x.dim() == 0 or x.shape[-1] != self.N:
+            raise ValueError(f"{type(self).__name__}: expected x.shape[-1] == {self.N}, "
+                             f"got {tuple(x.shape)}")
+        self.check_tensor("residual", residual, dtype=self.dtype, shape=x.shape)
+        self.check_tensor("weight", weight, numel=self.N)
+        self.check_tensor("bias", bias, numel=self.N)
         original_shape = x.shape
         rows = x.contiguous().reshape(-1, self.N)
         res = residual.contiguous().reshape(-1, self.N)

@@ -52,8 +52,7 @@ class ArgreduceKernel(Kernel):
         device_index: Accepted for API compatibility.
     """
 
-    supported_archs: Optional[list] = None
-    profile_kernel_name = "row_reduce_kernel"
+    profile_kernel_name = r"tileops\d+row_reduce_kernel"
 
     def __init__(
         self,
@@ -83,9 +82,11 @@ class ArgreduceKernel(Kernel):
                 "Reduction dimension is empty (N=0). "
                 "argmax/argmin over an empty dimension is undefined."
             )
-        return {"rows_per_wave": 1 if self.M >= 3072 else 0, "unroll": 4}
+        # row_reduce_kernel: as LogSumExpKernel
+        return {"wavefronts_per_row": 1 if self.M >= 3072 else 4, "packs_in_flight": 4}
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         _native.require_device(x)
+        self.check_tensor("x", x, dtype=self.dtype, shape=(self.M, self.N))
         x = x.contiguous()
         return _argreduce_fwd(self.M, self.N, self.op_kind, x)

@@ -47,8 +47,7 @@ class LogSumExpKernel(Kernel):
             per-device sizing).
     """
 
-    supported_archs: Optional[list] = None
-    profile_kernel_name = "row_reduce_kernel"
+    profile_kernel_name = r"tileops\d+row_reduce_kernel"
 
     def __init__(
         self,
@@ -71,10 +70,13 @@ class LogSumExpKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # wavefront per row when rows fill the chip, else 4 wavefronts per row
-        return {"rows_per_wave": 1 if self.M >= 3072 else 0, "unroll": 4}
+        # row_reduce_kernel: 256-thread workgroups; one wavefront per row
+        # (four rows per workgroup) from 3072 rows up, else the four
+        # wavefronts of a workgroup share a row; 4 packs in flight per lane
+        return {"wavefronts_per_row": 1 if self.M >= 3072 else 4, "packs_in_flight": 4}
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         _native.require_device(x)
+        self.check_tensor("x", x, dtype=self.dtype, shape=(self.M, self.N))
         x = x.contiguous()
         return _logsumexp_fwd(self.M, self.N, x)

@@ -15,7 +15,7 @@ from typing import Hashable, Optional, Union
 
 import torch
 
-from tileops.device import get_device_backend
+from tileops.device import HIPBackend, get_device_backend
 from tileops.kernels.kernel_base import Kernel
 
 
@@ -89,13 +89,15 @@ class Op(ABC):
 
 
 def _arch_supported(supported: Optional[list], backend: object) -> bool:
-    """True when the device ISA or marketing name contains a listed arch."""
-    if supported is None:
+    """True when the current device's ISA name (``gfx950:sramecc+:xnack-``
+    style) or marketing name contains a listed arch.  With no GPU (the host
+    backend) there is nothing to compare against: Ops can still be built (shapes, rooflines)
+    and any launch fails on its own for want of a device tensor."""
+    if supported is None or not backend.is_available() or not isinstance(backend, HIPBackend):
         return True
-    names = []
-    if backend.is_available():
-        names.append(backend.get_device_name(0))
-        arch = getattr(backend, "arch_name", None)
-        if arch is not None:
-            names.append(arch(0))
-    return any(str(a) in n for a in supported for n in names)
+    dev = backend.current_device()
+    names = [backend.get_device_name(dev)]
+    arch = getattr(backend, "arch_name", None)
+    if arch is not None:
+        names.append(arch(dev))
+    return any(str(a) in n for a in supported for n in names if n)

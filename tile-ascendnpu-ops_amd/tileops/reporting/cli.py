@@ -14,6 +14,7 @@ from pathlib import Path
 
 from tileops.reporting.report import write_reports
 from tileops.reporting.runner import list_operators, run_operator
+from tileops.reporting.session_timing import attach_session_timing
 
 
 def _parser() -> argparse.ArgumentParser:
@@ -38,7 +39,14 @@ def _parser() -> argparse.ArgumentParser:
     render = sub.add_parser("render", help="regenerate Markdown/HTML from run.json")
     render.add_argument("run_json")
     render.add_argument("--output-dir")
+    for p in (run, render):
+        p.add_argument("--with-session-timing", action="store_true",
+                       help="add the per-operator SESSION_TIMING_ANALYSIS.md totals")
     return ap
+
+
+def _package_root() -> Path:
+    return Path(__file__).resolve().parents[2]
 
 
 def main(argv: list[str] | None = None) -> int:
@@ -51,6 +59,8 @@ def main(argv: list[str] | None = None) -> int:
     if args.command == "render":
         src = Path(args.run_json).resolve()
         run = json.loads(src.read_text(encoding="utf-8"))
+        attach_session_timing(run, root=_package_root(), operator_catalog=list_operators(),
+                              enabled=args.with_session_timing)
         paths = write_reports(run, Path(args.output_dir).resolve() if args.output_dir else src.parent)
         print(f"Reports written to {paths['markdown']} and {paths['html']}")
         return 0
@@ -58,7 +68,8 @@ def main(argv: list[str] | None = None) -> int:
         "all" if args.all else args.op, test_file=args.test_file,
         benchmark_file=args.benchmark_file, prof_mode=args.prof_mode,
         kernel_name=args.kernel_name, reports_dir=args.reports_dir,
-        pytest_args=args.pytest_arg, timeout=args.timeout)
+        pytest_args=args.pytest_arg, timeout=args.timeout,
+        with_session_timing=args.with_session_timing)
     print(f"[tileops-report] status={run['status']} report={run_dir / 'report.md'}")
     return code
 

@@ -16,6 +16,8 @@ from copy import deepcopy
 from pathlib import Path
 from typing import Any
 
+from tileops.reporting.session_timing import format_duration
+
 _SHAPE_EXCLUDE = {"dtype", "dtypes", "op_params", "case_id", "label"}
 
 
@@ -138,6 +140,25 @@ def _perf_row(case: dict[str, Any]) -> list[str]:
             _fmt(case.get("bandwidth_tb_s")), _fmt(case.get("performance_tops"))]
 
 
+def _timing(run: dict[str, Any]) -> list[tuple[str, dict]]:
+    """(operator, record) pairs of an enabled session-timing section."""
+    st = run.get("session_timing") or {}
+    if not st.get("enabled"):
+        return []
+    return [(name, rec or {}) for name, rec in (st.get("operators") or {}).items()]
+
+
+def _timing_breakdown(rec: dict[str, Any]) -> str:
+    if rec.get("status") != "available":
+        return f"Timing data unavailable: {rec.get('reason') or rec.get('status', 'unknown')}"
+    parts = []
+    for b in rec.get("breakdown") or []:
+        ratio = b.get("ratio_percent")
+        pct = f" ({ratio:.2f}%)" if isinstance(ratio, (int, float)) else ""
+        parts.append(f"{b.get('name')}: {format_duration(b.get('duration_s'))}{pct}")
+    return "; ".join(parts) or "-"
+
+
 def render_markdown(run: dict[str, Any]) -> str:
     run = _normalize(run)
     s = run["summary"]
@@ -171,6 +192,12 @@ def render_markdown(run: dict[str, Any]) -> str:
         lines += ["| " + " | ".join(_cell(x) for x in _perf_row(c)) + " |" for c in cases]
         if not cases:
             lines.append("| - | No performance records |" + " - |" * (len(_PERF_HEAD) - 2))
+        lines.append("")
+    timing = _timing(run)
+    if timing:
+        lines += ["## Session Timing", "", "| Operator | Total Time | Breakdown |", "|---|---:|---|"]
+        lines += [f"| {_cell(name)} | {format_duration(rec.get('total_duration_s'))} | "
+                  f"{_cell(_timing_breakdown(rec))} |" for name, rec in timing]
         lines.append("")
     if run["warnings"]:
         lines += ["## Warnings", "", *(f"- {w}" for w in run["warnings"]), ""]
@@ -234,6 +261,12 @@ def render_html(run: dict[str, Any]) -> str:
         parts.append(f"<h3>{html.escape(str(op.get('operator')))}</h3>")
         parts.append(_table(list(_PERF_HEAD), [_perf_row(c) for c in cases], {1, 2, 3, 9, 10})
                      if cases else "<p>No performance records.</p>")
+    timing = _timing(run)
+    if timing:
+        parts.append("<h2>Session Timing / Session 耗时</h2>")
+        parts.append(_table(["Operator", "Total Time / 总时间", "Breakdown"],
+                            [[name, format_duration(rec.get("total_duration_s")),
+                              _timing_breakdown(rec)] for name, rec in timing], {1}))
     if run["warnings"]:
         parts.append("<h2>Warnings</h2><ul>" + "".join(
             f"<li>{html.escape(str(w))}</li>" for w in run["warnings"]) + "</ul>")

@@ -29,6 +29,7 @@ from tileops.manifest import load_manifest
 from tileops.reporting.analyzer import analyze_run
 from tileops.reporting.collector import load_benchmark_report, parse_junit_report
 from tileops.reporting.report import write_reports
+from tileops.reporting.session_timing import attach_session_timing
 from tileops.reporting.setup_info import collect_setup_info
 
 ALL_TESTS = "tests/ops"
@@ -178,6 +179,7 @@ def run_operator(
     pytest_args: list[str] | None = None,
     timeout: int | None = None,
     root: str | Path | None = None,
+    with_session_timing: bool = False,
 ) -> tuple[dict[str, Any], Path, int]:
     """Run one operator (or ``all``) and write its report directory.
 
@@ -258,6 +260,8 @@ def run_operator(
                       benchmark=benchmark, benchmark_exit_code=bench_code,
                       benchmark_tests=bench_tests, metadata=metadata, setup=setup,
                       operator_catalog=catalog)
+    attach_session_timing(run, root=Path(__file__).resolve().parents[2],
+                          operator_catalog=catalog, enabled=with_session_timing)
     write_reports(run, run_dir)
     (run_dir.parent / "latest.json").write_text(
         json.dumps({"run_id": run_dir.name, "run_json": str(run_dir / "run.json")}, indent=2),
