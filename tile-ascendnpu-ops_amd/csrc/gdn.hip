@@ -7,27 +7,30 @@
 // Chunked (C = 64 tokens) WY form.  Inside a chunk, with gc the cumulative
 // log-decay, G[l,s] = exp(gc_l - gc_s) (l >= s), A = strictly_lower(beta_l
 // G[l,s] k_l.k_s) and T = (I + A)^-1:
-//   w   = T diag(beta exp(gc)) k                 (C x K)   \  independent of S:
-//   Tu  = T diag(beta)                           (C x C)    > kernel 1, fully
-//   Aqk = scale * lower_incl(G o (q k^T))        (C x C)   /  parallel over chunks
-//   W   = Tu v - w S                                          \
-//   o   = scale exp(gc) o (q S) + Aqk W                        > kernel 2, sequential
-//   S  <- exp(gc_C) S + (exp(gc_C - gc) o k)^T W              /  over chunks
-// Only differences gc_l - gc_s <= 0, gc_C - gc_l <= 0 and gc <= 0 are ever
-// exponentiated, so nothing overflows however strong the decay.
+//   Tu  = T diag(beta)                                (C x C)   \ independent of S:
+//   Aqk = scale * lower_incl(G o (q k^T))             (C x C)   / kernel 1, parallel
+//   W   = Tu (v - exp(gc) o (k S))                              \
+//   o   = scale exp(gc) o (q S) + Aqk W                          > kernel 2, sequential
+//   S  <- exp(gc_C) S + k^T (exp(gc_C - gc) o W)                /  over chunks
+// (W = Tu v - w S with w = T diag(beta exp(gc)) k, regrouped so that the
+// recurrence multiplies k itself and kernel 1 hands over only two C x C
+// matrices and the per-token factors.)  Only differences gc_l - gc_s <= 0,
+// gc_C - gc_l <= 0 and gc <= 0 are ever exponentiated, so nothing overflows
+// however strong the decay.
 //
-// Kernel 1 (persistent, two workgroups per CU, the next chunk's q / k / g /
-// beta loaded while the current one is processed): K K^T and Q K^T on bf16
+// Kernel 1 (persistent, two workgroups per CU, the next chunk's q / k / g
+// / beta loaded while the current one is processed): K K^T and Q K^T on bf16
 // MFMA, the 64x64 unit-lower-triangular inverse in fp32 (16x16 diagonal
 // blocks by substitution, one wavefront each, the off-diagonal blocks by
-// products on fp32 MFMA), then w on bf16 MFMA.  -w, Tu, Aqk, the decayed
-// keys (k e^{gc_C - gc})^T and the per-token factors go to a workspace.
+// products on fp32 MFMA), Tu, Aqk and the factors to a 17 KB record per
+// chunk.
 // Kernel 2 (one workgroup per (b, h, 32-wide slice of V), 8 wavefronts):
 // four compute wavefronts keep the state slice in MFMA accumulators
-// (wavefront i owns key rows 32i..32i+31) and exchange its bf16 copy and W
-// through LDS; waves 0, 1 form W (rows 0-31, 32-63), waves 2, 3 the output
-// rows.  Four loader wavefronts bring the next chunk's operands into LDS
-// with direct-to-LDS loads meanwhile.  Two workgroup barriers per chunk.
+// (wavefront i owns key rows 32i..32i+31) and exchange its bf16 copy, U =
+// v - exp(gc) o (k S) and W through LDS; four loader wavefronts bring the
+// next chunk's k and record into LDS with direct-to-LDS loads meanwhile.
+// The output wavefronts read their q rows straight into registers.  Three
+// workgroup barriers per chunk.
 #include "common.h"
 
 namespace tileops {
@@ -35,6 +38,8 @@ namespace gdn {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int C = 64;    // chunk length
 constexpr int DK = 128;  // key dim
@@ -44,14 +49,14 @@ constexpr int KP = DK + 8;  // LDS row stride of a natural [C][DK] tile (element
 constexpr int CP = C + 8;   // LDS row stride of a transposed [*][C] tile (elements)
 constexpr float kLog2e = 1.4426950408889634f;
 
-// workspace per chunk
-constexpr size_t kWOff = 0;                                   // -w   [C][DK] bf16
-constexpr size_t kTuOff = kWOff + (size_t)C * DK * 2;         // Tu   [C][C]  bf16
-constexpr size_t kAqkOff = kTuOff + (size_t)C * C * 2;        // Aqk  [C][C]  bf16
-constexpr size_t kKdOff = kAqkOff + (size_t)C * C * 2;        // kd^T [DK][C] bf16
-constexpr size_t kFacOff = kKdOff + (size_t)DK * C * 2;       // factors, f32 [kFacN]
-constexpr int kFacN = 80;  // scale e^{gc_l} (l < C), e^{gc_C} at index C, zero pad
-constexpr size_t kChunkBytes = kFacOff + (size_t)kFacN * 4;
+// workspace record per chunk
+constexpr size_t kTuOff = 0;                                  // Tu   [C][C] bf16
+constexpr size_t kAqkOff = kTuOff + (size_t)C * C * 2;        // Aqk  [C][C] bf16
+constexpr size_t kFacOff = kAqkOff + (size_t)C * C * 2;       // factors, f32 [kFacN]
+constexpr int kFacN = 256;
+// factor slots: scale e^{gc_l}, e^{gc_l}, e^{gc_C - gc_l} (l < C), e^{gc_C}
+constexpr int kFacOut = 0, kFacG = C, kFacD = 2 * C, kFacChunk = 3 * C;
+constexpr size_t kChunkBytes = kFacOff + (size_t)kFacN * 4;  // 17,408
 
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -65,7 +70,7 @@ __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_e
 
 // Inclusive prefix sum over the 64 lanes of a wavefront by DPP lane moves,
 // with no LDS round trip (a shuffle-based scan waits on the LDS queue, which
-// the other workgroup of the CU keeps busy): Hillis-Steele inside each row
+// the other workgroups of the CU keep busy): Hillis-Steele inside each row
 // of 16 lanes (row_shr 1, 2, 4, 8; lanes shifted in from outside the row
 // read 0), then each row's total carried forward: row_bcast:15 adds lane
 // 16 r + 15 to row r + 1 (rows 1 and 3), row_bcast:31 adds lane 31 to rows
@@ -86,24 +91,6 @@ __device__ __forceinline__ float wave_inclusive_sum(float x) {
   return x;
 }
 
-// Store a 4-row x 8-column tile (4 packs of 8 bf16, one per row) transposed
-// into an LDS array with row stride `stride`: column d gets the 4 rows as one
-// 8-byte write at [d][r0].
-__device__ __forceinline__ void store_transposed4x8(bf16* dst, int stride, int d0, int r0,
-                                                    const u32x4 (&rows)[4]) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const uint32_t a0 = rows[0][m], a1 = rows[1][m], a2 = rows[2][m], a3 = rows[3][m];
-    const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
-    const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
-    const uint32_t hi01 = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
-    const uint32_t hi23 = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-    const int d = d0 + 2 * m;
-    *reinterpret_cast<uint2*>(dst + d * stride + r0) = make_uint2(lo01, lo23);
-    *reinterpret_cast<uint2*>(dst + (d + 1) * stride + r0) = make_uint2(hi01, hi23);
-  }
-}
-
 // Workgroup barrier that waits only for this wavefront's LDS accesses
 // (lgkmcnt(0); vmcnt and expcnt left at their maxima), so that global loads
 // and stores issued before it stay in flight across it (direct-to-LDS loads
@@ -117,19 +104,26 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Four fp32 values as four bf16 in one 8-byte word.
+__device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d) {
+  bf16 p[4] = {(bf16)a, (bf16)b, (bf16)c, (bf16)d};
+  return *reinterpret_cast<uint2*>(p);
+}
+
 // ---------------------------------------------------------------------------
 // kernel 1: per-chunk preparation
 // ---------------------------------------------------------------------------
-// LDS plan (two workgroups fit one CU):
+// LDS plan (three workgroups would fit one CU; two run per CU, so that the
+// kernel keeps every value in registers: at three the compiler spills):
 //   r0: k natural [C][KP] bf16 (K K^T)            -> T (fp32 [C][AS], inverse)
-//   r1: A^T fp32 [C][AS] (A^T[m][i] = A[i][m])    -> Tw, Tu (bf16 [C][CP] each)
-//   x_s: A21 T11 (fp32 32 x 32);  kT_s: k^T [d][c] bf16 (w);  aqk_s: Aqk bf16
+//   r1: A^T fp32 [C][AS] (A^T[m][i] = A[i][m])
+//   x_s: A10 T00 / A32 T22 / A21 T11 (fp32)
 constexpr int AS = 72;  // fp32 row stride of A^T / T (288 bytes: float4-aligned rows)
 constexpr int XS = 36;  // fp32 row stride of X
 
 // Global operands of one chunk for one thread, loaded a chunk ahead: k rows
 // 4vg..4vg+3 (dims 8vc..8vc+7), g / beta of token `lane`, and the q row this
-// wavefront's Q K^T block needs, in the MFMA A layout.  One uniform sequence
+// wavefront's Q K^T block needs, in the MFMA B layout.  One uniform sequence
 // for every wavefront (wave 3 loads q rows it does not use); rows past T load
 // the chunk's last row and are zeroed where they are consumed.
 struct PrepLoads {
@@ -145,16 +139,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(16))) float r0[C * AS];
   __shared__ __attribute__((aligned(16))) float r1[C * AS];
   __shared__ __attribute__((aligned(16))) float x_s[32 * XS];
-  __shared__ __attribute__((aligned(16))) bf16 kT_s[DK * CP];
-  __shared__ __attribute__((aligned(16))) bf16 aqk_s[C * CP];
-  __shared__ __attribute__((aligned(16))) float gc_s[C], beta_s[C], be_s[C], dec_s[C];
+  __shared__ __attribute__((aligned(16))) float gc_s[C], beta_s[C];
   static_assert(C * KP * 2 <= C * AS * 4, "k tile must fit the T region");
-  static_assert(2 * C * CP * 2 <= C * AS * 4, "Tw and Tu must fit the A region");
   bf16* k_s = reinterpret_cast<bf16*>(r0);
   float* t_s = r0;
   float* at_s = r1;
-  bf16* tw_s = reinterpret_cast<bf16*>(r1);
-  bf16* tu_s = tw_s + C * CP;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -191,42 +180,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int t0 = chunk * C;
     const int n = min(C, T - t0);
     uint8_t* wsc = ws + (size_t)blk * kChunkBytes;
-    bf16* w_ws = reinterpret_cast<bf16*>(wsc + kWOff);
     bf16* tu_ws = reinterpret_cast<bf16*>(wsc + kTuOff);
     bf16* aqk_ws = reinterpret_cast<bf16*>(wsc + kAqkOff);
-    bf16* kd_ws = reinterpret_cast<bf16*>(wsc + kKdOff);
     float* fac_ws = reinterpret_cast<float*>(wsc + kFacOff);
-    u32x4 (&kr)[4] = cur.kr;
 
-    // ---- stage k (natural + transposed); rows past T are 0
-    {
+    // ---- stage k; rows past T are 0
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 4 * vg + i;
-        if (row >= n) kr[i] = u32x4{0, 0, 0, 0};
-        *reinterpret_cast<u32x4*>(k_s + row * KP + vc * 8) = kr[i];
-      }
-      store_transposed4x8(kT_s, CP, vc * 8, 4 * vg, kr);
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * vg + i;
+      if (row >= n) cur.kr[i] = u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(k_s + row * KP + vc * 8) = cur.kr[i];
     }
-    if (wave == 0) {
+    if (wave == 3) {
       float x = lane < n ? cur.g : 0.0f;
       const float bt = lane < n ? cur.beta : 0.0f;
       x = wave_inclusive_sum(x);  // gc: inclusive prefix sum over the chunk
       gc_s[lane] = x;
       beta_s[lane] = bt;
-      be_s[lane] = bt * exp2f_fast(x * kLog2e);
-      // factors the recurrence applies: scale e^{gc} per output row, the
-      // chunk decay e^{gc_C}, and e^{gc_C - gc} for the decayed keys
-      const float gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), C - 1));
-      dec_s[lane] = exp2f_fast((gl - x) * kLog2e);
-      fac_ws[lane] = scale * exp2f_fast(x * kLog2e);
-      if (lane < kFacN - C) fac_ws[C + lane] = lane == 0 ? exp2f_fast(gl * kLog2e) : 0.0f;
+      // the factors the recurrence applies: scale e^{gc} per output row,
+      // e^{gc} on k S, e^{gc_C - gc} on W for the state update, e^{gc_C}
+      const float gl = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), C - 1));
+      const float eg = exp2f_fast(x * kLog2e);
+      fac_ws[kFacOut + lane] = scale * eg;
+      fac_ws[kFacG + lane] = eg;
+      fac_ws[kFacD + lane] = exp2f_fast((gl - x) * kLog2e);
+      fac_ws[kFacChunk + lane] = lane == 0 ? exp2f_fast(gl * kLog2e) : 0.0f;
     }
     lds_barrier();
 
-    // ---- K K^T -> A^T (fp32, LDS) and Q K^T -> Aqk (bf16, LDS), in 32x32
-    // blocks (row block rb, column block cb).  Only the strictly lower parts of
-    // the diagonal blocks and the block A21 of A are ever read back.
+    // ---- K K^T -> A^T (fp32, LDS) and Q K^T -> Aqk (bf16, to the record),
+    // in 32x32 blocks (row block rb, column block cb).  Only the strictly
+    // lower parts of the diagonal blocks and the block A21 of A are ever
+    // read back; the block l < 32 <= s of Aqk is zero.
     if (wave < 3) {
       // transposed orientation: k rows s of block cb as the A operand, k / q
       // rows l of block rb as B, so that a lane owns one row l (column of the
@@ -248,7 +234,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int s0 = cb * 32 + g4 * 8 + half * 4;
         const float4 gs4 = *reinterpret_cast<const float4*>(gc_s + s0);
         const float gsv[4] = {gs4.x, gs4.y, gs4.z, gs4.w};
-        bf16 q4[4];
+        float qv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = g4 * 4 + e;
@@ -259,29 +245,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           asm volatile("" : "+v"(gd));
           gd = sc <= l ? gd : 0.0f;
           at_s[sc * AS + l] = sc < l ? bel * gd * kk[r] : 0.0f;  // A^T[s][l]
-          q4[e] = (bf16)(scale * gd * qk[r]);
+          qv[e] = scale * gd * qk[r];
         }
-        *reinterpret_cast<uint2*>(aqk_s + l * CP + s0) = *reinterpret_cast<uint2*>(q4);
+        *reinterpret_cast<uint2*>(aqk_ws + l * C + s0) = pack_bf16x4(qv[0], qv[1], qv[2], qv[3]);
       }
-    } else {  // the block l < 32 <= s of Aqk is zero
+    } else {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4)
-        *reinterpret_cast<uint2*>(aqk_s + col * CP + 32 + g4 * 8 + half * 4) = make_uint2(0u, 0u);
+        *reinterpret_cast<uint2*>(aqk_ws + col * C + 32 + g4 * 8 + half * 4) = make_uint2(0u, 0u);
     }
     if (blk + gridDim.x < nblk) load(blk + gridDim.x, cur);  // operands consumed: next chunk
     lds_barrier();
 
-    // ---- Aqk rows to the workspace (16-byte stores); T = (I + A)^-1, blocked
-    // by 16: the four diagonal blocks Tbb by substitution (wave w: block w,
-    // lane j: column j; p[i] accumulates sum_m A[i][m] T[m][j]), then on fp32
-    // MFMA T10 = -T11 (A10 T00), T32 = -T33 (A32 T22) and, with 32-row
-    // blocks, T21 = -T22 (A21 T11).
-#pragma unroll
-    for (int e = tid; e < C * C / 8; e += 256) {
-      const int row = e >> 3, c8 = (e & 7) * 8;
-      *reinterpret_cast<u32x4*>(aqk_ws + row * C + c8) =
-          *reinterpret_cast<const u32x4*>(aqk_s + row * CP + c8);
-    }
+    // ---- T = (I + A)^-1, blocked by 16: the four diagonal blocks Tbb by
+    // substitution (wave w: block w, lane j: column j; p[i] accumulates
+    // sum_m A[i][m] T[m][j]), then on fp32 MFMA T10 = -T11 (A10 T00),
+    // T32 = -T33 (A32 T22) and, with 32-row blocks, T21 = -T22 (A21 T11).
     {
       const int base = 16 * wave, jl = lane & 15;
       float p[16];
@@ -373,78 +352,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     lds_barrier();
 
-    // ---- Tw = T diag(beta exp(gc)), Tu = T diag(beta) in bf16 (T12 is zero)
-    // (4 consecutive columns per thread: float4 in, 8-byte bf16 stores out)
+    // ---- Tu = T diag(beta) in bf16 to the record (T12 is zero); 4
+    // consecutive columns per thread: float4 in, one 8-byte store out
 #pragma unroll
     for (int e = tid; e < C * C / 4; e += 256) {
       const int i = e >> 4, j = (e & 15) * 4;
       const float4 t = (i < 32 && j >= 32) ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
                                            : *reinterpret_cast<const float4*>(t_s + i * AS + j);
-      const float4 be = *reinterpret_cast<const float4*>(be_s + j);
       const float4 bt = *reinterpret_cast<const float4*>(beta_s + j);
-      bf16 pw[4] = {(bf16)(t.x * be.x), (bf16)(t.y * be.y), (bf16)(t.z * be.z), (bf16)(t.w * be.w)};
-      bf16 pu[4] = {(bf16)(t.x * bt.x), (bf16)(t.y * bt.y), (bf16)(t.z * bt.z), (bf16)(t.w * bt.w)};
-      *reinterpret_cast<uint2*>(tw_s + i * CP + j) = *reinterpret_cast<uint2*>(pw);
-      *reinterpret_cast<uint2*>(tu_s + i * CP + j) = *reinterpret_cast<uint2*>(pu);
-    }
-    lds_barrier();
-
-    // ---- Tu rows to the workspace; -w^T = -(k^T Tw^T): wave -> 32-row block of
-    // d; the accumulator holds 4 consecutive d of one token row l (8 bytes),
-    // staged in the dead T region as [C][KP] bf16 so that the workspace rows
-    // are then written in whole 16-byte chunks (16 lanes per 256-byte row)
-#pragma unroll
-    for (int e = tid; e < C * C / 8; e += 256) {
-      const int row = e >> 3, c8 = (e & 7) * 8;
-      *reinterpret_cast<u32x4*>(tu_ws + row * C + c8) =
-          *reinterpret_cast<const u32x4*>(tu_s + row * CP + c8);
-    }
-    bf16* w_s = reinterpret_cast<bf16*>(r0);  // T is dead after the Tw / Tu conversion
-    {
-      const int db = wave;
-#pragma unroll
-      for (int lb = 0; lb < 2; ++lb) {
-        f32x16 aw = {};
-#pragma unroll
-        for (int ks = 0; ks < C / 16; ++ks) {
-          const bf16x8 ak = ld8(kT_s + (db * 32 + col) * CP + ks * 16 + half * 8);
-          const bf16x8 btw = ld8(tw_s + (lb * 32 + col) * CP + ks * 16 + half * 8);
-          aw = mfma(ak, btw, aw);
-        }
-        const int l = lb * 32 + col;
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          bf16 pw[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pw[e] = (bf16)(-aw[g4 * 4 + e]);
-          const int d = db * 32 + g4 * 8 + half * 4;
-          *reinterpret_cast<uint2*>(w_s + l * KP + d) = *reinterpret_cast<uint2*>(pw);
-        }
-      }
-    }
-    // ---- (decayed k)^T = (e^{gc_C - gc} o k)^T to the workspace, [DK][C]
-    // rows of 16-byte chunks (k rows past T are zero already)
-#pragma unroll
-    for (int j = 0; j < DK * C / 8 / 256; ++j) {
-      const int idx = tid + 256 * j;
-      const int d = idx >> 3, c8 = (idx & 7) * 8;
-      const bf16x8 kv = ld8(kT_s + d * CP + c8);
-      const float4 f0 = *reinterpret_cast<const float4*>(dec_s + c8);
-      const float4 f1 = *reinterpret_cast<const float4*>(dec_s + c8 + 4);
-      bf16x8 o8;
-      o8[0] = (bf16)((float)kv[0] * f0.x); o8[1] = (bf16)((float)kv[1] * f0.y);
-      o8[2] = (bf16)((float)kv[2] * f0.z); o8[3] = (bf16)((float)kv[3] * f0.w);
-      o8[4] = (bf16)((float)kv[4] * f1.x); o8[5] = (bf16)((float)kv[5] * f1.y);
-      o8[6] = (bf16)((float)kv[6] * f1.z); o8[7] = (bf16)((float)kv[7] * f1.w);
-      *reinterpret_cast<bf16x8*>(kd_ws + d * C + c8) = o8;
-    }
-    lds_barrier();
-#pragma unroll
-    for (int j = 0; j < C * DK / 8 / 256; ++j) {  // -w rows, [C][DK]
-      const int e = tid + 256 * j;
-      const int row = e >> 4, c8 = (e & 15) * 8;
-      *reinterpret_cast<u32x4*>(w_ws + row * DK + c8) =
-          *reinterpret_cast<const u32x4*>(w_s + row * KP + c8);
+      *reinterpret_cast<uint2*>(tu_ws + i * C + j) =
+          pack_bf16x4(t.x * bt.x, t.y * bt.y, t.z * bt.z, t.w * bt.w);
     }
     lds_barrier();  // LDS is rewritten by the next chunk
   }
@@ -460,12 +377,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // chunks XOR-swizzled by row, so that an MFMA operand read (16 consecutive
 // rows, one chunk each) touches 16 distinct bank groups.
 struct ChunkSlot {
-  bf16 w[C * DK];    // -w rows l: chunk p of row l holds chunk p ^ (l & 15)
+  bf16 k[C * DK];    // k rows l: chunk p of row l holds chunk p ^ (l & 15)
   bf16 q[C * DK];    // q rows, same swizzle
   bf16 tu[C * C];    // Tu rows: chunk p holds chunk p ^ ((l >> 1) & 7)
   bf16 aqk[C * C];   // Aqk rows, same
-  bf16 kd[DK * C];   // (decayed k)^T rows d, same
-  float fac[kFacN];  // scale e^{gc_l} (l < C), e^{gc_C} at [C]
+  bf16 v[C * VS];    // v slice rows [token][VS], unswizzled (read transposed)
+  float fac[kFacN];  // the record's factors
 };
 
 // element offset of 16-byte chunk `kc` of row `r` in a swizzled image with
@@ -474,10 +391,42 @@ __device__ __forceinline__ int swz16(int r, int kc) { return r * DK + ((kc ^ (r 
 __device__ __forceinline__ int swz8(int r, int kc) { return r * C + ((kc ^ ((r >> 1) & 7)) << 3); }
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void_ptr)p;
+}
+
+// Direct-to-LDS loads: lane l reads 16 (4) bytes at `base + off` (base
+// uniform, in SGPRs; off a per-lane byte offset) and they land at LDS byte
+// address lds + 16 l (4 l).  Issued as inline assembly so that the compiler
+// does not track the LDS writes: otherwise it waits for every outstanding
+// vector memory operation (the output stores included) before each LDS
+// access of the compute wavefronts.  Every wait for these loads is explicit
+// (vmcnt) and followed by a workgroup barrier before any wavefront reads
+// the data.
+// A wavefront-uniform pointer moved into SGPRs: both 32-bit halves are read
+// from the first active lane and joined as unsigned words (readfirstlane
+// returns int, which must not be sign-extended into the high word).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | (uint64_t)lo);
+}
+
+// The compiler's hazard checks do not look into inline assembly, so each
+// load starts with the wait states the ISA requires before it: 5 after a
+// VALU write (v_readfirstlane) of an SGPR the load reads (its base), 1
+// after the SALU write of M0.
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(uniform_ptr(base)),
+               "{m0}"(lds) : "memory");
+}
 
 // Fill the swizzled image `dst` (NCH 16-byte chunks, CPR per row) from the
-// rows `src + min(r, rmax) * stride` (elements).  Each of the 4 wavefronts
-// issues every 4th 1 KB window (64 chunks).
+// rows `src + min(r, rmax) * stride` (elements; `src` uniform).  Each of the
+// 4 wavefronts issues every 4th 1 KB window (64 chunks).
 template <int CPR, int NCH>
 __device__ __forceinline__ void gather_rows(bf16* dst, const bf16* src, int64_t stride, int rmax,
                                             int wave, int lane) {
@@ -487,24 +436,25 @@ __device__ __forceinline__ void gather_rows(bf16* dst, const bf16* src, int64_t 
     const int win = 4 * i + wave;
     const int ch = win * 64 + lane;
     const int r = ch / CPR, p = ch % CPR;
-    const int key = CPR == 16 ? (r & 15) : ((r >> 1) & 7);
-    const bf16* g = src + (int64_t)min(r, rmax) * stride + ((p ^ key) << 3);
-    __builtin_amdgcn_global_load_lds(g, (lds_void_ptr)(dst + win * 512), 16, 0, 0);
+    const int key = CPR == 16 ? (r & 15) : CPR == 8 ? ((r >> 1) & 7) : 0;
+    const uint32_t off = (uint32_t)(((int64_t)min(r, rmax) * stride + ((p ^ key) << 3)) * 2);
+    lds_dma16(src, off, lds_addr(dst + win * 512));
   }
 }
 
 __global__ __launch_bounds__(512) void gdn_recur_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ v, const float* __restrict__ h0,
-    const uint8_t* __restrict__ ws, bf16* __restrict__ o, float* __restrict__ hT, int B, int T,
-    int H, int NC) {
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ h0, const uint8_t* __restrict__ ws, bf16* __restrict__ o,
+    float* __restrict__ hT, int B, int T, int H, int NC) {
   constexpr int SP = DK + 8;  // row stride of S^T [v][d]
   // two separate objects, so that the compiler can tell a slot being read
   // from the one the direct-to-LDS loads are filling
   __shared__ __attribute__((aligned(16))) ChunkSlot slot0;
   __shared__ __attribute__((aligned(16))) ChunkSlot slot1;
   __shared__ __attribute__((aligned(16))) bf16 st_s[VS * SP];      // bf16 S^T (slice)
-  __shared__ __attribute__((aligned(16))) bf16 wt_s[VS * CP];      // bf16 W^T (slice)
-  __shared__ __attribute__((aligned(16))) bf16 vt_s[2][VS * CP];   // v^T (slice)
+  __shared__ __attribute__((aligned(16))) bf16 ut_s[VS * CP];      // U^T (slice)
+  __shared__ __attribute__((aligned(16))) bf16 wt_s[VS * CP];      // W^T (slice)
+  __shared__ __attribute__((aligned(16))) bf16 dwt_s[VS * CP];     // (e^{gc_C - gc} o W)^T
   __shared__ __attribute__((aligned(16))) uint32_t touch_s[64];    // landing area of L2 prefetches
 
   // waves 0-3 compute; waves 4-7 (one per SIMD beside them) only move the
@@ -515,7 +465,8 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
   const int lw = wave & 3;     // index among the loaders / among the compute waves
   const int ltid = tid & 255;  // thread index inside its group of four wavefronts
   const int col = lane & 31, half = lane >> 5;
-  // the VS-slices of one head run on the same XCD (they share q, w, Aqk, kd)
+  // the VS-slices of one head run on the same XCD (they share q, k and the
+  // chunk records through its L2)
   const int total = gridDim.x;
   int id = blockIdx.x;
   if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
@@ -527,65 +478,105 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
   const int64_t tok_stride = (int64_t)H * DK;
   const int rblk = wave & 1;         // chunk rows 32*rblk .. 32*rblk+31 (A operands)
   const int arow = rblk * 32 + col;  // A-operand row of this lane
-  const int vrow = ltid >> 2, vcol = (ltid & 3) * 8;
 
-  // chunk c's operands (loader wavefronts): the LDS images of slot `sl`
-  // (direct loads) and this thread's 16 bytes of the v slice (register,
-  // transposed into LDS later)
-  auto load = [&](int c, ChunkSlot& sl, u32x4& vr) {
+  // k^T (A operand of the state update) through transpose reads of the
+  // natural k image: in each group of 16 lanes, lane j points at 4 dims
+  // (d0 + 4 (j % 4) ..) of token row t0 + j / 4 and receives dim d0 + j of
+  // those 4 tokens.  Lane group g covers dims 32 wave + 16 (g & 1) .. and
+  // tokens 8 (g >> 1) .. of each 16-token step; the second read takes the
+  // next 4 tokens.  The swizzle key (t & 15) does not depend on the step, so
+  // the step is a constant 16-row (4 KB) offset.
+  int ktoff[2] = {0, 0};
+  if (!loader) {
+    const int g16 = lane >> 4, j16 = lane & 15;
+    const int dd = 32 * wave + 16 * (g16 & 1) + 4 * (j16 & 3);
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+      const int t = 8 * (g16 >> 1) + 4 * rd + (j16 >> 2);
+      ktoff[rd] = t * DK + (((dd >> 3) ^ (t & 15)) << 3) + (dd & 7);
+    }
+  }
+  // v^T (columns of the natural v image) for the U update: 4 consecutive
+  // token rows (32 rblk + 8 g4 + 4 half ..) of v column `col`, by the same
+  // transpose read: lane j of a 16-lane group points at 4 columns
+  // (16 (g & 1) + 4 (j % 4) ..) of token row 4 (g >> 1) + j / 4 (+ the g4
+  // and rblk terms, constants of 8 and 32 rows).
+  int vtoff = 0;
+  {
+    const int g16 = lane >> 4, j16 = lane & 15;
+    vtoff = (32 * rblk + 4 * (g16 >> 1) + (j16 >> 2)) * VS + 16 * (g16 & 1) + 4 * (j16 & 3);
+  }
+  auto read_vt4 = [&](const bf16* vimg, int g4) -> uint2 {
+    const uint32_t a = lds_addr(vimg) + (uint32_t)((vtoff + g4 * 8 * VS) * 2);
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)a));
+  };
+  auto read_kt = [&](const bf16* kimg, int ks) -> bf16x8 {
+    const uint32_t base = lds_addr(kimg) + (uint32_t)(ks * 16 * DK * 2);
+    const v4i16 x0 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(base + ktoff[0] * 2));
+    const v4i16 x1 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(base + ktoff[1] * 2));
+    const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
+    const u32x4 w4 = {y0.x, y0.y, y1.x, y1.y};
+    return __builtin_bit_cast(bf16x8, w4);
+  };
+
+  // chunk c's operands (loader wavefronts), all by direct-to-LDS loads into
+  // the images of slot `sl`, in two parts so that the CU's load path is busy
+  // in two phases of a step rather than one: the q and k rows, then the
+  // record and the v slice.
+  // Rows past T are clamped onto the chunk's last row rather than zeroed:
+  // their k only meets columns of Tu and rows of W that are exactly zero
+  // (beta = 0 there), their v only those columns of Tu, and their q only
+  // output rows that are not stored.
+  auto load_rows = [&](int c, ChunkSlot& sl) {
     const int t0 = c * C;
-    const int last = min(C, T - t0) - 1;  // rows past T read the last row (see below)
+    const int last = min(C, T - t0) - 1;
+    const int64_t row0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK;
+    gather_rows<16, C * DK / 8>(sl.k, k + row0, tok_stride, last, lw, lane);
+    gather_rows<16, C * DK / 8>(sl.q, q + row0, tok_stride, last, lw, lane);
+  };
+  auto load_record = [&](int c, ChunkSlot& sl) {
+    const int t0 = c * C;
+    const int last = min(C, T - t0) - 1;
     const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
-    // Rows past T are clamped onto the chunk's last row rather than zeroed:
-    // their q only reaches output rows that are not stored, and their v only
-    // meets columns of Tu that are exactly zero (beta = 0).
-    vr = *reinterpret_cast<const u32x4*>(
-        v + ((int64_t)b * T + t0 + min(vrow, last)) * tok_stride + (int64_t)h * DV + v0 + vcol);
-    gather_rows<16, C * DK / 8>(sl.w, reinterpret_cast<const bf16*>(wsc + kWOff), DK, C - 1, lw,
-                                lane);
-    gather_rows<16, C * DK / 8>(sl.q, q + ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK,
-                                tok_stride, last, lw, lane);
+    const int64_t row0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DV;
     gather_rows<8, C * C / 8>(sl.tu, reinterpret_cast<const bf16*>(wsc + kTuOff), C, C - 1, lw,
                               lane);
-    gather_rows<8, C * C / 8>(sl.aqk, reinterpret_cast<const bf16*>(wsc + kAqkOff), C, C - 1, lw,
-                              lane);
-    gather_rows<8, DK * C / 8>(sl.kd, reinterpret_cast<const bf16*>(wsc + kKdOff), C, DK - 1, lw,
-                               lane);
-    if (lw == 0 && lane < kFacN / 4)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const float*>(wsc + kFacOff) + lane * 4,
-                                       (lds_void_ptr)sl.fac, 16, 0, 0);
+    gather_rows<8, C * C / 8>(sl.aqk, reinterpret_cast<const bf16*>(wsc + kAqkOff), C, C - 1,
+                              lw, lane);
+    gather_rows<VS / 8, C * VS / 8>(sl.v, v + row0 + v0, tok_stride, last, lw, lane);
+    if (lw == 0) lds_dma16(wsc + kFacOff, (uint32_t)lane * 16, lds_addr(sl.fac));
   };
   // L2 prefetch of chunk c (loader wavefronts): one 4-byte load per 128-byte
-  // line of its workspace record and q rows (the four V-slices of a head
+  // line of its record and of its q and k rows (the four V-slices of a head
   // share them, every fourth line each) and of this slice's v rows, landing
   // in a scratch LDS word.  Every thread issues exactly one (spare threads
   // repeat a line), so the wait counts stay exact.
   auto touch = [&](int c) {
     constexpr int kWsLines = (int)((kChunkBytes + 127) / 128);
-    constexpr int kShared = kWsLines + 2 * C;  // + q rows, two lines each
+    constexpr int kShared = kWsLines + 4 * C;  // + q and k rows, two lines each
     constexpr int kPerSlice = (kShared + 3) / 4;
+    static_assert(kPerSlice + C <= 256, "one prefetch per loader thread");
     const int t0 = c * C;
     const int last = min(C, T - t0) - 1;
     const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
+    const int64_t row0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK;
     const void* a;
     const int j = min(ltid, kPerSlice - 1) * 4 + vs;
     if (ltid < kPerSlice && j < kShared) {
-      a = j < kWsLines ? static_cast<const void*>(wsc + (size_t)j * 128)
-                       : static_cast<const void*>(
-                             q + ((int64_t)b * T + t0 + min((j - kWsLines) >> 1, last)) *
-                                     tok_stride +
-                             (int64_t)h * DK + ((j - kWsLines) & 1) * 64);
+      if (j < kWsLines) {
+        a = wsc + (size_t)j * 128;
+      } else {
+        const int r = j - kWsLines;  // 4 lines per token row: q then k, two halves each
+        a = ((r & 2) ? k : q) + row0 + (int64_t)min(r >> 2, last) * tok_stride + (r & 1) * 64;
+      }
     } else {
       const int r = min(max(ltid - kPerSlice, 0), C - 1);
-      a = v + ((int64_t)b * T + t0 + min(r, last)) * tok_stride + (int64_t)h * DV + v0;
+      a = v + row0 + (int64_t)min(r, last) * tok_stride + v0;
     }
-    __builtin_amdgcn_global_load_lds(a, (lds_void_ptr)touch_s, 4, 0, 0);
-  };
-  // v^T of a loaded chunk into LDS slot `buf`
-  auto stage_v = [&](const u32x4& vr, int buf) {
-    const bf16* ve = reinterpret_cast<const bf16*>(&vr);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) vt_s[buf][(vcol + j) * CP + vrow] = ve[j];
+    asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, off" : : "v"(a), "{m0}"(lds_addr(touch_s))
+                 : "memory");
   };
 
   // state rows of a compute wave: d = 32 * wave + (r / 4) * 8 + half * 4 + r % 4
@@ -600,28 +591,38 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
   auto publish_state = [&]() {
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      bf16 p[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = (bf16)s_acc[g4 * 4 + e];
       const int d = 32 * wave + g4 * 8 + half * 4;
-      *reinterpret_cast<uint2*>(st_s + col * SP + d) = *reinterpret_cast<uint2*>(p);
+      *reinterpret_cast<uint2*>(st_s + col * SP + d) =
+          pack_bf16x4(s_acc[g4 * 4 + 0], s_acc[g4 * 4 + 1], s_acc[g4 * 4 + 2], s_acc[g4 * 4 + 3]);
+    }
+  };
+  // a 32-row block of a [token][v] accumulator (rows 32 rblk + ..; lane: v
+  // column `col`) as bf16 into the transposed image [v][token], each value
+  // scaled by the factor of its token row
+  auto put_rows_t = [&](bf16* img, const f32x16& acc, const float* fac) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int cl = rblk * 32 + g4 * 8 + half * 4;
+      const float4 f = fac ? *reinterpret_cast<const float4*>(fac + cl)
+                           : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+      *reinterpret_cast<uint2*>(img + col * CP + cl) =
+          pack_bf16x4(acc[g4 * 4 + 0] * f.x, acc[g4 * 4 + 1] * f.y, acc[g4 * 4 + 2] * f.z,
+                      acc[g4 * 4 + 3] * f.w);
     }
   };
 
-  // one chunk: `cur` holds its operands (and vt_s[c & 1], st_s); the loader
-  // wavefronts fill `nxt` and vt_s[(c + 1) & 1] meanwhile
+  // one chunk: `cur` holds its operands (and st_s); the loader wavefronts
+  // fill `nxt` meanwhile
   auto step = [&](int c, const ChunkSlot& cur, ChunkSlot& nxt) {
-    const int buf = c & 1;
-    const bool more = c + 1 < NC;
     if (loader) {
       // chunk c + 1 into `nxt` (past the end: the last chunk again, never
-      // read); after v^T is staged, the L2 prefetch of chunk c + 2.  Both are
-      // unconditional so that the wait counts stay exact
-      u32x4 vr;
-      load(more ? c + 1 : NC - 1, nxt, vr);
-      lds_barrier();  // (barrier B)
-      if (more) stage_v(vr, buf ^ 1);
+      // read), then the L2 prefetch of chunk c + 2.  Both are unconditional
+      // so that the wait counts stay exact
+      load_rows(min(c + 1, NC - 1), nxt);
+      lds_barrier();  // (barrier U)
+      load_record(min(c + 1, NC - 1), nxt);
       touch(min(c + 2, NC - 1));
+      lds_barrier();  // (barrier W)
       // a wavefront's counters cover only its own loads: each loader waits
       // for its share of the next chunk's images (everything but the one
       // prefetch issued last: vmcnt(1)) before the barrier
@@ -632,38 +633,52 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
     const int t0 = c * C;
     const int n = min(C, T - t0);
 
-    // waves 0, 1: W = Tu v - w S (rows 32 rblk ..); waves 2, 3: the output
-    // in the transposed orientation, o^T = S^T q^T (tokens 32 rblk ..), so
-    // that a lane owns one token: its row factor is one scalar and its 16
-    // values are 4 runs of 4 consecutive v, stored straight to memory
+    // waves 0, 1: P = k S (token rows 32 rblk ..), then U = v - e^{gc} o P;
+    // waves 2, 3: the output in the transposed orientation, o^T = S^T q^T
+    // (tokens 32 rblk ..), so that a lane owns one token: its row factor is
+    // one scalar and its 16 values are 4 runs of 4 consecutive v, stored
+    // straight to memory
     f32x16 acc = {};
     if (wave < 2) {
 #pragma unroll
-      for (int ks = 0; ks < C / 16; ++ks)
-        acc = mfma(ld8(cur.tu + swz8(arow, ks * 2 + half)),
-                   ld8(vt_s[buf] + col * CP + ks * 16 + half * 8), acc);
-#pragma unroll
       for (int ks = 0; ks < DK / 16; ++ks)
-        acc = mfma(ld8(cur.w + swz16(arow, ks * 2 + half)),
+        acc = mfma(ld8(cur.k + swz16(arow, ks * 2 + half)),
                    ld8(st_s + col * SP + ks * 16 + half * 8), acc);
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        bf16 p[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) p[e] = (bf16)acc[g4 * 4 + e];
         const int cl = rblk * 32 + g4 * 8 + half * 4;
-        *reinterpret_cast<uint2*>(wt_s + col * CP + cl) = *reinterpret_cast<uint2*>(p);
+        const float4 eg = *reinterpret_cast<const float4*>(cur.fac + kFacG + cl);
+        const uint2 vw = read_vt4(cur.v, g4);  // v[cl .. cl + 3][v0 + col]
+        const bf16* vv = reinterpret_cast<const bf16*>(&vw);
+        *reinterpret_cast<uint2*>(ut_s + col * CP + cl) =
+            pack_bf16x4(fmaf(-eg.x, acc[g4 * 4 + 0], (float)vv[0]),
+                        fmaf(-eg.y, acc[g4 * 4 + 1], (float)vv[1]),
+                        fmaf(-eg.z, acc[g4 * 4 + 2], (float)vv[2]),
+                        fmaf(-eg.w, acc[g4 * 4 + 3], (float)vv[3]));
       }
     } else {
 #pragma unroll
       for (int ks = 0; ks < DK / 16; ++ks)
         acc = mfma(ld8(st_s + col * SP + ks * 16 + half * 8),
                    ld8(cur.q + swz16(arow, ks * 2 + half)), acc);
-      const float f = cur.fac[arow];  // scale e^{gc} of this lane's token
+      const float f = cur.fac[kFacOut + arow];  // scale e^{gc} of this lane's token
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] *= f;
     }
-    lds_barrier();  // (barrier B) W^T visible
+    lds_barrier();  // (barrier U) U^T visible
+
+    if (wave < 2) {  // W = Tu U; Tu is lower triangular: row block 0 needs tokens < 32 only
+      f32x16 wacc = {};
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        if (rblk == 0 && ks >= 2) break;
+        wacc = mfma(ld8(cur.tu + swz8(arow, ks * 2 + half)),
+                    ld8(ut_s + col * CP + ks * 16 + half * 8), wacc);
+      }
+      put_rows_t(wt_s, wacc, nullptr);
+      put_rows_t(dwt_s, wacc, cur.fac + kFacD);
+    }
+    lds_barrier();  // (barrier W) W^T and the decayed W^T visible
 
     if (wave >= 2) {  // o^T += W^T Aqk^T, then this lane's token row to memory
 #pragma unroll
@@ -673,30 +688,25 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
       if (arow < n) {
         bf16* orow = o + ((int64_t)b * T + t0 + arow) * tok_stride + (int64_t)h * DV + v0;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          bf16 p[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) p[e] = (bf16)acc[g4 * 4 + e];
-          *reinterpret_cast<uint2*>(orow + g4 * 8 + half * 4) = *reinterpret_cast<uint2*>(p);
-        }
+        for (int g4 = 0; g4 < 4; ++g4)
+          *reinterpret_cast<uint2*>(orow + g4 * 8 + half * 4) =
+              pack_bf16x4(acc[g4 * 4 + 0], acc[g4 * 4 + 1], acc[g4 * 4 + 2], acc[g4 * 4 + 3]);
       }
     }
-    // S <- exp(gc_C) S + (decayed k)^T W   (rows 32 * wave .. of the state)
-    const float dec = cur.fac[C];
+    // S <- e^{gc_C} S + k^T (e^{gc_C - gc} o W)   (rows 32 * wave .. of the state)
+    const float dec = cur.fac[kFacChunk];
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_acc[r] *= dec;
 #pragma unroll
     for (int ks = 0; ks < C / 16; ++ks)
-      s_acc = mfma(ld8(cur.kd + swz8(32 * wave + col, ks * 2 + half)),
-                   ld8(wt_s + col * CP + ks * 16 + half * 8), s_acc);
+      s_acc = mfma(read_kt(cur.k, ks), ld8(dwt_s + col * CP + ks * 16 + half * 8), s_acc);
     publish_state();
     lds_barrier();  // (barrier A) next chunk's images, S^T and v^T visible
   };
 
   if (NC > 0 && loader) {
-    u32x4 vr;
-    load(0, slot0, vr);
-    stage_v(vr, 0);
+    load_rows(0, slot0);
+    load_record(0, slot0);
     touch(min(1, NC - 1));
     __builtin_amdgcn_s_waitcnt(0x0F71);
   }
@@ -757,10 +767,11 @@ extern "C" int tileops_gdn_prefill_fwd(const void* q, const void* k, const void*
   const bf16* qb = static_cast<const bf16*>(q);
   const bf16* kb = static_cast<const bf16*>(k);
   if (nblk > 0)
-    gdn::gdn_prep_kernel<<<dim3((unsigned)std::min<int64_t>(nblk, 2 * device_cu_count())), dim3(256), 0, s>>>(
-        qb, kb, g, beta, static_cast<uint8_t*>(ws), (int)B, (int)T, (int)H, nc, scale);
+    gdn::gdn_prep_kernel<<<dim3((unsigned)std::min<int64_t>(nblk, 2 * device_cu_count())),
+                           dim3(256), 0, s>>>(qb, kb, g, beta, static_cast<uint8_t*>(ws), (int)B,
+                                              (int)T, (int)H, nc, scale);
   gdn::gdn_recur_kernel<<<dim3((unsigned)(B * H * (gdn::DV / gdn::VS))), dim3(512), 0, s>>>(
-      qb, static_cast<const bf16*>(v), h0, static_cast<const uint8_t*>(ws),
+      qb, kb, static_cast<const bf16*>(v), h0, static_cast<const uint8_t*>(ws),
       static_cast<bf16*>(o), hT, (int)B, (int)T, (int)H, nc);
   return launch_status();
 }
