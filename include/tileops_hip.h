@@ -227,6 +227,24 @@ size_t tileops_gdn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t H, int6
                                            int64_t V, int64_t chunk);
 
 /*
+ * tileops_gdn_prefill_fwd without a workspace argument, for callers that
+ * cannot allocate device memory (code under stream capture, serving loops,
+ * harnesses that forbid allocation): it allocates nothing and calls no
+ * allocating routine.  No counterpart in the reference.  The per-chunk
+ * records live in a 16 MiB device array of the library (one per GPU, held
+ * until the process ends), filled segment by segment, so any T works and
+ * B * H is limited to 963 (one 17 KiB record per head must fit; larger
+ * B * H returns TILEOPS_EWORKSPACE).  Every call on a GPU shares that
+ * array: calls that overlap on one GPU (concurrent streams, threads) race.
+ * Results equal tileops_gdn_prefill_fwd's bit for bit.
+ */
+int tileops_gdn_prefill_fwd_noalloc(const void* q, const void* k, const void* v,
+                                    const float* g, const float* beta, const float* h0,
+                                    void* o, float* hT, int64_t B, int64_t T, int64_t H,
+                                    int64_t K, int64_t V, int64_t chunk, float scale,
+                                    int dtype, void* stream);
+
+/*
  * Single-token gated linear attention decode, layout BHD, per (b, h):
  *   new_state[dk][dv] = exp(gk[dk]) * state[dk][dv] + k[dk] * v[dv]
  *   o[dv]             = scale * sum_dk q[dk] * new_state[dk][dv]

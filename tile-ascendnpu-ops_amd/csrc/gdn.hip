@@ -31,6 +31,9 @@
 // next chunk's k and record into LDS with direct-to-LDS loads meanwhile.
 // The output wavefronts read their q rows straight into registers.  Three
 // workgroup barriers per chunk.
+#include <algorithm>
+#include <mutex>
+
 #include "common.h"
 
 namespace tileops {
@@ -134,7 +137,7 @@ struct PrepLoads {
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ g,
-    const float* __restrict__ beta, uint8_t* __restrict__ ws, int B, int T, int H, int NC,
+    const float* __restrict__ beta, uint8_t* __restrict__ ws, int B, int T, int H, int c0, int NS,
     float scale) {
   __shared__ __attribute__((aligned(16))) float r0[C * AS];
   __shared__ __attribute__((aligned(16))) float r1[C * AS];
@@ -152,10 +155,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int qrow = rb * 32 + col;
   const int vg = tid & 15, vc = tid >> 4;
   const int64_t tok_stride = (int64_t)H * DK;  // DK == DV
-  const uint64_t nblk = (uint64_t)B * H * NC;
+  // record blk of the workspace: (b, h) = blk / NS, chunk c0 + blk % NS
+  const uint64_t nblk = (uint64_t)B * H * NS;
 
   auto load = [&](uint64_t blk, PrepLoads& L) {
-    const int chunk = (int)(blk % NC), bh = (int)(blk / NC);
+    const int chunk = c0 + (int)(blk % NS), bh = (int)(blk / NS);
     const int h = bh % H, b = bh / H;
     const int t0 = chunk * C, n = min(C, T - t0);
     const bf16* kb = k + ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK + vc * 8;
@@ -176,7 +180,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   uint64_t blk = blockIdx.x;
   if (blk < nblk) load(blk, cur);
   for (; blk < nblk; blk += gridDim.x) {
-    const int chunk = (int)(blk % NC);
+    const int chunk = c0 + (int)(blk % NS);
     const int t0 = chunk * C;
     const int n = min(C, T - t0);
     uint8_t* wsc = ws + (size_t)blk * kChunkBytes;
@@ -442,10 +446,15 @@ __device__ __forceinline__ void gather_rows(bf16* dst, const bf16* src, int64_t 
   }
 }
 
+// The kernel runs chunks c0 .. c1 - 1 of every head, reading their records
+// at (b H + h) NS + (c - c0) of the workspace, starting from state h0 (zero
+// when null) and leaving the state in hT.  h0 may be hT itself (a segment
+// continuing the previous one): each workgroup reads its own state slice
+// before its first chunk and writes it after its last.
 __global__ __launch_bounds__(512) void gdn_recur_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const float* __restrict__ h0, const uint8_t* __restrict__ ws, bf16* __restrict__ o,
-    float* __restrict__ hT, int B, int T, int H, int NC) {
+    const float* h0, const uint8_t* __restrict__ ws, bf16* __restrict__ o, float* hT, int B,
+    int T, int H, int c0, int c1, int NS) {
   constexpr int SP = DK + 8;  // row stride of S^T [v][d]
   // two separate objects, so that the compiler can tell a slot being read
   // from the one the direct-to-LDS loads are filling
@@ -539,7 +548,7 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
   auto load_record = [&](int c, ChunkSlot& sl) {
     const int t0 = c * C;
     const int last = min(C, T - t0) - 1;
-    const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
+    const uint8_t* wsc = ws + (((size_t)b * H + h) * NS + (c - c0)) * kChunkBytes;
     const int64_t row0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DV;
     gather_rows<8, C * C / 8>(sl.tu, reinterpret_cast<const bf16*>(wsc + kTuOff), C, C - 1, lw,
                               lane);
@@ -560,7 +569,7 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
     static_assert(kPerSlice + C <= 256, "one prefetch per loader thread");
     const int t0 = c * C;
     const int last = min(C, T - t0) - 1;
-    const uint8_t* wsc = ws + (((size_t)b * H + h) * NC + c) * kChunkBytes;
+    const uint8_t* wsc = ws + (((size_t)b * H + h) * NS + (c - c0)) * kChunkBytes;
     const int64_t row0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK;
     const void* a;
     const int j = min(ltid, kPerSlice - 1) * 4 + vs;
@@ -618,10 +627,10 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
       // chunk c + 1 into `nxt` (past the end: the last chunk again, never
       // read), then the L2 prefetch of chunk c + 2.  Both are unconditional
       // so that the wait counts stay exact
-      load_rows(min(c + 1, NC - 1), nxt);
+      load_rows(min(c + 1, c1 - 1), nxt);
       lds_barrier();  // (barrier U)
-      load_record(min(c + 1, NC - 1), nxt);
-      touch(min(c + 2, NC - 1));
+      load_record(min(c + 1, c1 - 1), nxt);
+      touch(min(c + 2, c1 - 1));
       lds_barrier();  // (barrier W)
       // a wavefront's counters cover only its own loads: each loader waits
       // for its share of the next chunk's images (everything but the one
@@ -704,20 +713,20 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
     lds_barrier();  // (barrier A) next chunk's images, S^T and v^T visible
   };
 
-  if (NC > 0 && loader) {
-    load_rows(0, slot0);
-    load_record(0, slot0);
-    touch(min(1, NC - 1));
+  if (c1 > c0 && loader) {
+    load_rows(c0, slot0);
+    load_record(c0, slot0);
+    touch(min(c0 + 1, c1 - 1));
     __builtin_amdgcn_s_waitcnt(0x0F71);
   }
   if (!loader) publish_state();
   lds_barrier();
-  int c = 0;
-  for (; c + 1 < NC; c += 2) {
+  int c = c0;
+  for (; c + 1 < c1; c += 2) {
     step(c, slot0, slot1);
     step(c + 1, slot1, slot0);
   }
-  if (c < NC) step(c, slot0, slot1);
+  if (c < c1) step(c, slot0, slot1);
 
   if (loader) {
     __builtin_amdgcn_s_waitcnt(0);  // no load may land after the workgroup's LDS is released
@@ -735,11 +744,92 @@ __global__ __launch_bounds__(512) void gdn_recur_kernel(
 
 using namespace tileops;
 
+namespace tileops {
+namespace gdn {
+
+// Workspace bytes for `nchunks` chunks of each of B * H heads.
+inline size_t records_bytes(int64_t BH, int64_t nchunks) {
+  return (size_t)(BH * nchunks) * kChunkBytes;
+}
+
+// Argument checks shared by the entry points (0 when the call may proceed).
+static int check_args(const void* q, const void* k, const void* v, const float* g,
+                      const float* beta, const void* o, const float* hT, int64_t B, int64_t T,
+                      int64_t H, int64_t K, int64_t V, int64_t chunk, int dtype) {
+  if (B < 0 || T < 0 || H <= 0) return TILEOPS_ESHAPE;
+  if (K != DK || V != DV || chunk != C) return TILEOPS_ESHAPE;
+  if (B > 65535 || H > 65535 || T > INT32_MAX / 2) return TILEOPS_ESHAPE;
+  if (dtype != TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (B == 0) return 0;
+  if (!hT) return TILEOPS_ENULL;
+  if (T > 0) {
+    if (!q || !k || !v || !g || !beta || !o) return TILEOPS_ENULL;
+    if (!host_aligned16(q) || !host_aligned16(k) || !host_aligned16(v)) return TILEOPS_EINVAL;
+  }
+  const int64_t nc = (T + C - 1) / C;
+  if (B * H * nc > (int64_t)UINT32_MAX || B * H * (DV / VS) > INT32_MAX) return TILEOPS_ESHAPE;
+  return 0;
+}
+
+// The whole prefill in segments of `seg` chunks: per segment the parallel
+// preparation into `ws` (records of seg chunks per head), then the
+// recurrence over the segment, the state carried from one segment to the
+// next in hT.  One segment when `ws` holds every chunk's record.
+static int run_segments(const bf16* q, const bf16* k, const bf16* v, const float* g,
+                        const float* beta, const float* h0, bf16* o, float* hT, int B, int T,
+                        int H, float scale, uint8_t* ws, int seg, hipStream_t s) {
+  const int nc = (T + C - 1) / C;
+  const unsigned rgrid = (unsigned)(B * H * (DV / VS));
+  if (nc == 0) {  // no chunk: the state passes through
+    gdn_recur_kernel<<<dim3(rgrid), dim3(512), 0, s>>>(q, k, v, h0, ws, o, hT, B, T, H, 0, 0, 1);
+    return launch_status();
+  }
+  for (int c0 = 0; c0 < nc; c0 += seg) {
+    const int ns = std::min(seg, nc - c0);
+    const int64_t nblk = (int64_t)B * H * ns;
+    gdn_prep_kernel<<<dim3((unsigned)std::min<int64_t>(nblk, 2 * device_cu_count())), dim3(256),
+                      0, s>>>(q, k, g, beta, ws, B, T, H, c0, ns, scale);
+    gdn_recur_kernel<<<dim3(rgrid), dim3(512), 0, s>>>(q, k, v, c0 == 0 ? h0 : hT, ws, o, hT, B,
+                                                      T, H, c0, c0 + ns, ns);
+    if (int e = launch_status()) return e;
+  }
+  return 0;
+}
+
+// Scratch of the allocation-free entry point: every call on a GPU shares
+// that GPU's copy (the last call's records stay in it), so calls that
+// overlap on one GPU race.  kScratchBytes bounds the heads per call: one
+// chunk record per head must fit, B * H <= 963.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device: in host code the array's name is only a stand-in symbol.
+static int scratch_ptr(uint8_t** out) {
+  static std::mutex mu;
+  static uint8_t* ptrs[64] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= 64) return TILEOPS_EINVAL;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    ptrs[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = ptrs[dev];
+  return 0;
+}
+
+}  // namespace gdn
+}  // namespace tileops
+
 extern "C" size_t tileops_gdn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K,
                                                       int64_t V, int64_t chunk) {
   if (B < 0 || T < 0 || H < 0 || K != gdn::DK || V != gdn::DV || chunk != gdn::C) return 0;
-  const int64_t nc = (T + gdn::C - 1) / gdn::C;
-  return (size_t)(B * H * nc) * gdn::kChunkBytes;
+  return gdn::records_bytes(B * H, (T + gdn::C - 1) / gdn::C);
 }
 
 extern "C" int tileops_gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* g,
@@ -747,31 +837,36 @@ extern "C" int tileops_gdn_prefill_fwd(const void* q, const void* k, const void*
                                        int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
                                        int64_t chunk, float scale, int dtype, void* ws,
                                        size_t ws_bytes, void* stream) {
-  if (B < 0 || T < 0 || H <= 0) return TILEOPS_ESHAPE;
-  if (K != gdn::DK || V != gdn::DV || chunk != gdn::C) return TILEOPS_ESHAPE;
-  if (B > 65535 || H > 65535 || T > INT32_MAX / 2) return TILEOPS_ESHAPE;
-  if (dtype != TILEOPS_BF16) return TILEOPS_EINVAL;
+  if (int e = gdn::check_args(q, k, v, g, beta, o, hT, B, T, H, K, V, chunk, dtype)) return e;
   if (B == 0) return 0;
-  if (!hT) return TILEOPS_ENULL;
   const size_t need = tileops_gdn_prefill_workspace_bytes(B, T, H, K, V, chunk);
-  if (T > 0) {
-    if (!q || !k || !v || !g || !beta || !o) return TILEOPS_ENULL;
-    if (!ws || ws_bytes < need) return TILEOPS_EWORKSPACE;
-    if (!host_aligned16(q) || !host_aligned16(k) || !host_aligned16(v) || !host_aligned16(ws))
-      return TILEOPS_EINVAL;
+  if (T > 0 && (!ws || ws_bytes < need || !host_aligned16(ws))) {
+    if (ws && !host_aligned16(ws)) return TILEOPS_EINVAL;
+    return TILEOPS_EWORKSPACE;
   }
   const int nc = (int)((T + gdn::C - 1) / gdn::C);
-  const int64_t nblk = B * H * nc;
-  if (nblk > (int64_t)UINT32_MAX) return TILEOPS_ESHAPE;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bf16* qb = static_cast<const bf16*>(q);
-  const bf16* kb = static_cast<const bf16*>(k);
-  if (nblk > 0)
-    gdn::gdn_prep_kernel<<<dim3((unsigned)std::min<int64_t>(nblk, 2 * device_cu_count())),
-                           dim3(256), 0, s>>>(qb, kb, g, beta, static_cast<uint8_t*>(ws), (int)B,
-                                              (int)T, (int)H, nc, scale);
-  gdn::gdn_recur_kernel<<<dim3((unsigned)(B * H * (gdn::DV / gdn::VS))), dim3(512), 0, s>>>(
-      qb, kb, static_cast<const bf16*>(v), h0, static_cast<const uint8_t*>(ws),
-      static_cast<bf16*>(o), hT, (int)B, (int)T, (int)H, nc);
-  return launch_status();
+  return gdn::run_segments(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                           static_cast<const bf16*>(v), g, beta, h0, static_cast<bf16*>(o), hT,
+                           (int)B, (int)T, (int)H, scale, static_cast<uint8_t*>(ws),
+                           nc > 0 ? nc : 1, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tileops_gdn_prefill_fwd_noalloc(const void* q, const void* k, const void* v,
+                                               const float* g, const float* beta,
+                                               const float* h0, void* o, float* hT, int64_t B,
+                                               int64_t T, int64_t H, int64_t K, int64_t V,
+                                               int64_t chunk, float scale, int dtype,
+                                               void* stream) {
+  if (int e = gdn::check_args(q, k, v, g, beta, o, hT, B, T, H, K, V, chunk, dtype)) return e;
+  if (B == 0) return 0;
+  const int64_t per_chunk = B * H * (int64_t)gdn::kChunkBytes;  // one chunk of every head
+  if (per_chunk > (int64_t)gdn::kScratchBytes) return TILEOPS_EWORKSPACE;
+  uint8_t* ws = nullptr;
+  if (int e = gdn::scratch_ptr(&ws)) return e;
+  const int nc = (int)((T + gdn::C - 1) / gdn::C);
+  const int seg = (int)std::min<int64_t>(std::max(nc, 1), (int64_t)gdn::kScratchBytes / per_chunk);
+  return gdn::run_segments(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                           static_cast<const bf16*>(v), g, beta, h0, static_cast<bf16*>(o), hT,
+                           (int)B, (int)T, (int)H, scale, ws, seg,
+                           static_cast<hipStream_t>(stream));
 }

@@ -77,6 +77,14 @@ SIGNATURES = {
         ctypes.c_size_t,
         [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64],
     ),
+    "tileops_gdn_prefill_fwd_noalloc": (
+        _c_int,
+        [
+            _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+            _c_float, _c_int, _c_p,
+        ],
+    ),
     "tileops_bitwise_not_fwd": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
     "tileops_add_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_float, _c_int, _c_p]),
     "tileops_lerp_fwd": (
