@@ -12,11 +12,17 @@ also carries:
                 kernel time comes from HIP events on the launch stream over
                 the timed region (one launch per step), ``traffic`` from the
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/
-  cpu_baseline  the CPU oracle of the same operator on the host, one core
+  cpu_baseline  the reference's own reference program of the same operator
+                (its torch ``ref_program``, restated in oracle/torch_ref.py)
+                on the host's CPU share, timed on a bounded sample
   suite         every other benchmark configuration (elementwise,
                 predicates, FusedAddLayerNorm, LogSumExp, Argmax, MHA fwd
                 causal / non-causal, GDN prefill) with its own roofline
-                fraction
+                fraction and its own CPU-baseline figure
+
+``--only NAME[,NAME...]`` runs just those operators (suite names, or
+GeluAndMulFwdOp for the headline) and prints their entries: the form the
+committed rocprofv3 summaries under profiles/ are recorded with.
 
 Only one GPU is used; ``--gpus`` above 1 exits with an explanation.
 """
@@ -107,33 +113,145 @@ def bench_headline(steps: int, warmup: int) -> dict:
     }
 
 
-def cpu_baseline_gelu(M: int, N: int) -> dict:
-    """The CPU oracle of GeluAndMul (numpy + scipy erf, one thread) over the
-    whole workload in 2048-row chunks; GB/s of the same algorithmic bytes."""
-    import numpy as np
+def cpu_threads() -> int:
+    """Threads of the host's CPU share: OMP_NUM_THREADS when set (the GPU
+    hosts set it to the cores a GPU is given), else the affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover - non-Linux
+        return os.cpu_count() or 1
 
-    from oracle import tileops_oracle as orc
 
-    rng = np.random.default_rng(1235)
-    chunk = 2048
-    elapsed = 0.0
-    rows = 0
-    for r0 in range(0, M, chunk):
-        x = orc.round_to("bfloat16", rng.standard_normal((chunk, 2 * N), dtype=np.float32))
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def _median_s(fn, reps: int = 3) -> float:
+    """Median wall time of ``reps`` calls after one warm-up call."""
+    fn()
+    times = []
+    for _ in range(reps):
         t0 = time.perf_counter()
-        orc.gelu_and_mul(x, "bfloat16")
-        elapsed += time.perf_counter() - t0
-        rows += chunk
-    nbytes = 3 * rows * N * 2
-    return {
-        "value": round(nbytes / elapsed / 1e9, 4),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"full workload, {rows} rows of bf16 x[*, {2 * N}] in {chunk}-row chunks "
-        f"({elapsed:.1f} s, numpy/scipy oracle, single thread; host has "
-        f"{os.cpu_count()} cores)",
-    }
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def cpu_baselines(only=None) -> dict:
+    """The reference programs (oracle/torch_ref.py) on the CPU: torch's
+    intra-op pool with the host's CPU share, the median of 3 runs after a
+    warm-up, on a bounded sample of each benchmark workload; rates in the
+    unit of the GPU figure (GB/s of algorithmic bytes, TFLOP/s)."""
+    from oracle import torch_ref as tr
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(1235)
+    out = {}
+
+    def want(name):
+        return only is None or name in only
+
+    def entry(value, unit, sample):
+        return {"value": round(value, 4), "unit": unit, "sample": sample}
+
+    if want("GeluAndMulFwdOp") or want("GeluTanhAndMulFwdOp"):
+        rows, n = 2048, 11008
+        x = torch.randn(rows, 2 * n, generator=gen).bfloat16()
+        nbytes = 3 * rows * n * 2
+        for name, fn in (("GeluAndMulFwdOp", tr.gelu_and_mul),
+                         ("GeluTanhAndMulFwdOp", tr.gelu_tanh_and_mul)):
+            if want(name):
+                t = _median_s(lambda: fn(x))
+                out[name] = entry(nbytes / t / 1e9, "GB/s",
+                                  f"{rows} of the 16384 rows of bf16 x[16384, 22016]")
+        del x
+    shape = (8192, 8192)
+    n = shape[0] * shape[1]
+    if any(want(k) for k in ("HardswishFwdOp", "HardsigmoidFwdOp", "ClampScalarFwdOp")):
+        x = (torch.randn(shape, generator=gen) * 3).half()
+        for name, fn in (("HardswishFwdOp", tr.hardswish), ("HardsigmoidFwdOp", tr.hardsigmoid),
+                         ("ClampScalarFwdOp", lambda t: tr.clamp_scalar(t, -1.0, 1.0))):
+            if want(name):
+                t = _median_s(lambda: fn(x))
+                out[name] = entry(4 * n / t / 1e9, "GB/s", "the whole fp16 x[8192, 8192]")
+        del x
+    if any(want(k) for k in ("IsnanFwdOp", "IsinfFwdOp", "IsfiniteFwdOp")):
+        x = torch.randn(shape, generator=gen)
+        idx = torch.randperm(n, generator=gen)[: n // 50]
+        x.view(-1)[idx[: n // 100]] = float("inf")
+        x.view(-1)[idx[n // 100:]] = float("nan")
+        for name, fn in (("IsnanFwdOp", tr.isnan), ("IsinfFwdOp", tr.isinf),
+                         ("IsfiniteFwdOp", tr.isfinite)):
+            if want(name):
+                t = _median_s(lambda: fn(x))
+                out[name] = entry(5 * n / t / 1e9, "GB/s", "the whole fp32 x[8192, 8192]")
+        del x
+    if want("FusedAddLayerNormFwdOp"):
+        rows, hid = 4096, 4096
+        x = torch.randn(rows, hid, generator=gen).bfloat16()
+        r = torch.randn(rows, hid, generator=gen).bfloat16()
+        w = 1 + 0.1 * torch.randn(hid, generator=gen)
+        b = 0.1 * torch.randn(hid, generator=gen)
+        t = _median_s(lambda: tr.fused_add_layer_norm(x, r, w, b, 1e-5))
+        out["FusedAddLayerNormFwdOp"] = entry((4 * rows * hid * 2 + 2 * hid * 4) / t / 1e9,
+                                              "GB/s", f"{rows} of the 32768 rows")
+        del x, r
+    if want("LogSumExpFwdOp") or want("ArgmaxFwdOp"):
+        rows, cols = 8192, 4096
+        x = torch.randn(rows, cols, generator=gen) * 2.0
+        if want("LogSumExpFwdOp"):
+            t = _median_s(lambda: tr.logsumexp(x))
+            out["LogSumExpFwdOp"] = entry((rows * cols + rows) * 4 / t / 1e9, "GB/s",
+                                          f"{rows} of the 32768 rows")
+        if want("ArgmaxFwdOp"):
+            t = _median_s(lambda: tr.argmax(x))
+            out["ArgmaxFwdOp"] = entry((rows * cols * 4 + rows * 8) / t / 1e9, "GB/s",
+                                       f"{rows} of the 32768 rows")
+        del x
+    for causal in (False, True):
+        name = f"MultiHeadAttentionFwdOp[causal={causal}]"
+        if not want(name) and not want("MultiHeadAttentionFwdOp"):
+            continue
+        S, D, heads = 4096, 128, 2
+        q, k, v = (torch.randn(1, S, heads, D, generator=gen).bfloat16() for _ in range(3))
+        t = _median_s(lambda: tr.mha_fwd(q, k, v, causal), reps=1)
+        flops = 4 * heads * S * S * D / (2 if causal else 1)
+        out[name] = entry(flops / t / 1e12, "TFLOP/s",
+                          f"{heads} of the 256 (batch, head) pairs (SDPA in fp32); the rate "
+                          "holds for all 256, which are independent")
+    if want("GatedDeltaNetPrefillFwdOp"):
+        B, T, H, K = 4, 512, 16, 128
+        q = F_normalize(torch.randn(B, T, H, K, generator=gen)).bfloat16()
+        k = F_normalize(torch.randn(B, T, H, K, generator=gen)).bfloat16()
+        v = torch.randn(B, T, H, K, generator=gen).bfloat16()
+        g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gen))
+        beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+        t = _median_s(lambda: tr.gdn_sequential(q, k, v, g, beta, K**-0.5), reps=1)
+        C = 64
+        flops = (6 * C * C * K + 4 * C * C * K + 6 * C * K * K + C**3 // 3) * (T // C) * B * H
+        out["GatedDeltaNetPrefillFwdOp"] = entry(
+            flops / t / 1e12, "TFLOP/s",
+            f"the first {T} of the 8192 tokens of every (batch, head) (the token "
+            "recurrence's work grows linearly in T), counted with the chunked-form flops")
+    cores = {"threads": threads, "host_cpus": os.cpu_count(), "cpu": _cpu_model()}
+    for v in out.values():
+        v.update(cores)
+    return out
+
+
+def F_normalize(x: torch.Tensor) -> torch.Tensor:
+    return torch.nn.functional.normalize(x, dim=-1)
 
 
 # ---------------------------------------------------------------------------
@@ -163,7 +281,7 @@ def _mfma_entry(name, op, args_list, flops, steps, warmup, workload):
     }
 
 
-def bench_suite(steps: int, warmup: int) -> dict:
+def bench_suite(steps: int, warmup: int, only=None) -> dict:
     from tileops.ops.attention import MultiHeadAttentionFwdOp
     from tileops.ops.elementwise import (
         ClampScalarFwdOp,
@@ -183,82 +301,101 @@ def bench_suite(steps: int, warmup: int) -> dict:
     torch.manual_seed(1235)
     dev = "cuda"
 
+    def want(*names):
+        return only is None or any(nm in only for nm in names)
+
     # elementwise family, fp16 [8192, 8192] ~ N(0, 3^2)
     shape = (8192, 8192)
     n = shape[0] * shape[1]
-    rot = _rotations(4 * n)
-    xs = [ScaledNormalWorkload(shape, torch.float16, 3.0).gen_inputs() for _ in range(rot)]
-    for name, op in (
-        ("HardswishFwdOp", HardswishFwdOp(n, torch.float16)),
-        ("HardsigmoidFwdOp", HardsigmoidFwdOp(n, torch.float16)),
-        ("ClampScalarFwdOp", ClampScalarFwdOp(n, torch.float16, min=-1.0, max=1.0)),
-    ):
-        k, v = _mem_entry(name, op, xs, op.eval_roofline()[1], steps, warmup,
-                          "fp16 x[8192, 8192] ~ N(0, 9)")
-        out[k] = v
-        _log(f"{k}: {v}")
-    del xs
+    unary = ("HardswishFwdOp", "HardsigmoidFwdOp", "ClampScalarFwdOp")
+    if want(*unary):
+        rot = _rotations(4 * n)
+        xs = [ScaledNormalWorkload(shape, torch.float16, 3.0).gen_inputs() for _ in range(rot)]
+        for name, op in (
+            ("HardswishFwdOp", HardswishFwdOp(n, torch.float16)),
+            ("HardsigmoidFwdOp", HardsigmoidFwdOp(n, torch.float16)),
+            ("ClampScalarFwdOp", ClampScalarFwdOp(n, torch.float16, min=-1.0, max=1.0)),
+        ):
+            if want(name):
+                k, v = _mem_entry(name, op, xs, op.eval_roofline()[1], steps, warmup,
+                                  "fp16 x[8192, 8192] ~ N(0, 9)")
+                out[k] = v
+                _log(f"{k}: {v}")
+        del xs
 
     # predicates, fp32 [8192, 8192], 1% +-inf and 1% NaN at random positions
-    rot = _rotations(5 * n)
-    xs = [ScatteredSpecialWorkload(shape, torch.float32).gen_inputs() for _ in range(rot)]
-    for name, op in (
-        ("IsnanFwdOp", IsnanFwdOp(n, torch.float32)),
-        ("IsinfFwdOp", IsinfFwdOp(n, torch.float32)),
-        ("IsfiniteFwdOp", IsfiniteFwdOp(n, torch.float32)),
-    ):
-        k, v = _mem_entry(name, op, xs, op.eval_roofline()[1], steps, warmup,
-                          "fp32 x[8192, 8192], 1% +-inf, 1% NaN")
-        out[k] = v
-        _log(f"{k}: {v}")
-    del xs
+    preds = ("IsnanFwdOp", "IsinfFwdOp", "IsfiniteFwdOp")
+    if want(*preds):
+        rot = _rotations(5 * n)
+        xs = [ScatteredSpecialWorkload(shape, torch.float32).gen_inputs() for _ in range(rot)]
+        for name, op in (
+            ("IsnanFwdOp", IsnanFwdOp(n, torch.float32)),
+            ("IsinfFwdOp", IsinfFwdOp(n, torch.float32)),
+            ("IsfiniteFwdOp", IsfiniteFwdOp(n, torch.float32)),
+        ):
+            if want(name):
+                k, v = _mem_entry(name, op, xs, op.eval_roofline()[1], steps, warmup,
+                                  "fp32 x[8192, 8192], 1% +-inf, 1% NaN")
+                out[k] = v
+                _log(f"{k}: {v}")
+        del xs
 
     # GeluTanhAndMul, same shape as the headline
-    M, N = 16384, 11008
-    x = torch.randn(M, 2 * N, device=dev, dtype=torch.bfloat16)
-    op = GeluTanhAndMulFwdOp(M, N, torch.bfloat16)
-    k, v = _mem_entry("GeluTanhAndMulFwdOp", op, [(x,)], op.eval_roofline()[1], steps, warmup,
-                      "bf16 x[16384, 22016] ~ N(0, 1)")
-    out[k] = v
-    _log(f"{k}: {v}")
-    del x
+    if want("GeluTanhAndMulFwdOp"):
+        M, N = 16384, 11008
+        x = torch.randn(M, 2 * N, device=dev, dtype=torch.bfloat16)
+        op = GeluTanhAndMulFwdOp(M, N, torch.bfloat16)
+        k, v = _mem_entry("GeluTanhAndMulFwdOp", op, [(x,)], op.eval_roofline()[1], steps,
+                          warmup, "bf16 x[16384, 22016] ~ N(0, 1)")
+        out[k] = v
+        _log(f"{k}: {v}")
+        del x
 
     # FusedAddLayerNorm, bf16 [32768, 4096], fp32 gamma / beta
-    wl = FusedAddLayerNormWorkload(32768, 4096, torch.bfloat16, param_dtype=torch.float32)
-    inputs = wl.gen_inputs()
-    op = FusedAddLayerNormFwdOp(dtype=torch.bfloat16, eps=1e-5)
-    op(*inputs)
-    k, v = _mem_entry("FusedAddLayerNormFwdOp", op, [inputs], op.eval_roofline()[1], steps,
-                      warmup, "bf16 x, residual [32768, 4096]; fp32 gamma ~ N(1, 0.01), "
-                      "beta ~ N(0, 0.01); eps 1e-5")
-    out[k] = v
-    _log(f"{k}: {v}")
-    del inputs
+    if want("FusedAddLayerNormFwdOp"):
+        wl = FusedAddLayerNormWorkload(32768, 4096, torch.bfloat16, param_dtype=torch.float32)
+        inputs = wl.gen_inputs()
+        op = FusedAddLayerNormFwdOp(dtype=torch.bfloat16, eps=1e-5)
+        op(*inputs)
+        k, v = _mem_entry("FusedAddLayerNormFwdOp", op, [inputs], op.eval_roofline()[1], steps,
+                          warmup, "bf16 x, residual [32768, 4096]; fp32 gamma ~ N(1, 0.01), "
+                          "beta ~ N(0, 0.01); eps 1e-5")
+        out[k] = v
+        _log(f"{k}: {v}")
+        del inputs
 
     # LogSumExp / Argmax, fp32 [32768, 4096] ~ N(0, 4)
-    x = torch.randn(32768, 4096, device=dev) * 2.0
-    for name, op in (("LogSumExpFwdOp", LogSumExpFwdOp(dtype=torch.float32, dim=-1)),
-                     ("ArgmaxFwdOp", ArgmaxFwdOp(dtype=torch.float32, dim=-1))):
-        op(x)
-        k, v = _mem_entry(name, op, [(x,)], op.eval_roofline()[1], steps, warmup,
-                          "fp32 x[32768, 4096] ~ N(0, 4), dim=-1")
-        out[k] = v
-        _log(f"{k}: {v}")
-    del x
+    if want("LogSumExpFwdOp", "ArgmaxFwdOp"):
+        x = torch.randn(32768, 4096, device=dev) * 2.0
+        for name, op in (("LogSumExpFwdOp", LogSumExpFwdOp(dtype=torch.float32, dim=-1)),
+                         ("ArgmaxFwdOp", ArgmaxFwdOp(dtype=torch.float32, dim=-1))):
+            if want(name):
+                op(x)
+                k, v = _mem_entry(name, op, [(x,)], op.eval_roofline()[1], steps, warmup,
+                                  "fp32 x[32768, 4096] ~ N(0, 4), dim=-1")
+                out[k] = v
+                _log(f"{k}: {v}")
+        del x
 
     # MHA forward, bf16 BSHD (8, 4096, 32, 128)
-    B, S, H, D = 8, 4096, 32, 128
-    q, kk, vv = (torch.randn(B, S, H, D, device=dev, dtype=torch.bfloat16) for _ in range(3))
-    for causal in (False, True):
-        op = MultiHeadAttentionFwdOp(B, H, S, D, causal, torch.bfloat16)
-        name = f"MultiHeadAttentionFwdOp[causal={causal}]"
-        k, v = _mfma_entry(name, op, [(q, kk, vv)], op.eval_roofline()[0], max(3, steps // 4),
-                           max(1, warmup // 2), "bf16 q, k, v (8, 4096, 32, 128) BSHD, "
-                           "scale 1/sqrt(128)")
-        out[k] = v
-        _log(f"{k}: {v}")
-    del q, kk, vv
+    mha = ("MultiHeadAttentionFwdOp[causal=False]", "MultiHeadAttentionFwdOp[causal=True]")
+    if want("MultiHeadAttentionFwdOp", *mha):
+        B, S, H, D = 8, 4096, 32, 128
+        q, kk, vv = (torch.randn(B, S, H, D, device=dev, dtype=torch.bfloat16) for _ in range(3))
+        for causal in (False, True):
+            name = f"MultiHeadAttentionFwdOp[causal={causal}]"
+            if not want(name, "MultiHeadAttentionFwdOp"):
+                continue
+            op = MultiHeadAttentionFwdOp(B, H, S, D, causal, torch.bfloat16)
+            k, v = _mfma_entry(name, op, [(q, kk, vv)], op.eval_roofline()[0],
+                               max(3, steps // 4), max(1, warmup // 2),
+                               "bf16 q, k, v (8, 4096, 32, 128) BSHD, scale 1/sqrt(128)")
+            out[k] = v
+            _log(f"{k}: {v}")
+        del q, kk, vv
 
+    if not want("GatedDeltaNetPrefillFwdOp"):
+        return out
     try:
         from tileops.ops.linear_attention import GatedDeltaNetPrefillFwdOp
         from tileops.workloads.linear_attention import GdnPrefillWorkload
@@ -285,6 +422,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", help="comma-separated operators to run (profiling); prints "
+                    "their entries only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (counter calibration for "
                     "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -313,11 +452,41 @@ def main() -> int:
 
     # stdout carries the one JSON line only: everything the operators print
     # while they are built and run goes to stderr
+    only = set(args.only.split(",")) if args.only else None
     with contextlib.redirect_stdout(sys.stderr):
-        head = bench_headline(args.steps, args.warmup)
-        _log(f"headline GeluAndMulFwdOp: {head['gbs']:.1f} GB/s, {head['kernel_ms'] * 1e3:.1f} us")
-        suite = {} if args.no_suite else bench_suite(args.steps, args.warmup)
-        cpu = None if args.no_cpu_baseline else cpu_baseline_gelu(head["M"], head["N"])
+        if only is not None:
+            res = {}
+            if "GeluAndMulFwdOp" in only:
+                h = bench_headline(args.steps, args.warmup)
+                res["GeluAndMulFwdOp"] = {"us": round(h["kernel_ms"] * 1e3, 2),
+                                          "GB/s": round(h["gbs"], 1),
+                                          "frac": round(h["gbs"] / HBM_PEAK_GBS, 4)}
+            res.update(bench_suite(args.steps, args.warmup, only))
+            if not args.no_cpu_baseline:
+                for name, c in cpu_baselines(only).items():
+                    res.setdefault(name, {})["cpu"] = c
+        else:
+            head = bench_headline(args.steps, args.warmup)
+            _log(f"headline GeluAndMulFwdOp: {head['gbs']:.1f} GB/s, "
+                 f"{head['kernel_ms'] * 1e3:.1f} us")
+            suite = {} if args.no_suite else bench_suite(args.steps, args.warmup)
+            cpus = {} if args.no_cpu_baseline else cpu_baselines(
+                None if not args.no_suite else {"GeluAndMulFwdOp"})
+            for name, c in cpus.items():
+                if name in suite:
+                    suite[name]["cpu"] = c
+            hc = cpus.get("GeluAndMulFwdOp")
+            cpu = None if hc is None else {
+                "value": hc["value"], "unit": hc["unit"], "cores": hc["threads"],
+                "kind": "port",
+                "sample": f"the reference's reference program (torch, "
+                f"tests/ops/test_gelu_and_mul.py:63-77, restated in oracle/torch_ref.py) on "
+                f"{hc['sample']}, median of 3 runs after a warm-up, {hc['threads']} threads "
+                f"of a {hc['host_cpus']}-CPU host ({hc['cpu']})",
+            }
+    if only is not None:
+        print(json.dumps({"only": sorted(only), "results": res}), flush=True)
+        return 0
 
     line = {
         "metric": METRIC,

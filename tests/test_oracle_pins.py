@@ -442,3 +442,62 @@ def test_gdn_empty_sequence_passes_state_through():
     o, s = orc.gdn_sequential(q, k, v, g, beta, s0, 1.0)
     assert o.shape == (2, 0, 2, 6)
     np.testing.assert_allclose(s, s0, rtol=1e-6)
+
+
+# -- the torch reference programs bench.py times as the CPU baseline ---------------------
+def test_torch_reference_programs_match_the_oracle():
+    from oracle import torch_ref as tr
+
+    rng = np.random.default_rng(21)
+    x16 = torch.from_numpy((rng.standard_normal((64, 96)) * 3).astype(np.float32)).half()
+    xn = x16.float().numpy()
+    assert np.array_equal(tr.hardswish(x16).float().numpy(), orc.hardswish(xn, "float16"))
+    assert np.array_equal(tr.hardsigmoid(x16).float().numpy(), orc.hardsigmoid(xn, "float16"))
+    assert np.array_equal(tr.clamp_scalar(x16, -1.0, 1.0).float().numpy(),
+                          orc.clamp_scalar(xn, "float16", -1.0, 1.0))
+    xs = rng.standard_normal((32, 64)).astype(np.float32)
+    xs[0, :3] = [np.nan, np.inf, -np.inf]
+    for fn in ("isnan", "isinf", "isfinite"):
+        assert np.array_equal(getattr(tr, fn)(torch.from_numpy(xs)).numpy(), getattr(orc, fn)(xs))
+    xg = torch.from_numpy(rng.standard_normal((16, 256)).astype(np.float32)).bfloat16()
+    for fn in ("gelu_and_mul", "gelu_tanh_and_mul"):
+        np.testing.assert_allclose(getattr(tr, fn)(xg).float().numpy(),
+                                   getattr(orc, fn)(xg.float().numpy(), "bfloat16"),
+                                   rtol=1.6e-2, atol=1.6e-2)
+    xl = torch.from_numpy(rng.standard_normal((8, 128)).astype(np.float32)).bfloat16()
+    rl = torch.from_numpy(rng.standard_normal((8, 128)).astype(np.float32)).bfloat16()
+    w = torch.from_numpy((1 + 0.1 * rng.standard_normal(128)).astype(np.float32))
+    b = torch.from_numpy((0.1 * rng.standard_normal(128)).astype(np.float32))
+    y, added = tr.fused_add_layer_norm(xl, rl, w, b, 1e-5)
+    y_ref, added_ref = orc.fused_add_layer_norm(xl.float().numpy(), rl.float().numpy(),
+                                                w.numpy(), b.numpy(), 1e-5, "bfloat16")
+    assert np.array_equal(added.float().numpy(), added_ref)
+    np.testing.assert_allclose(y.float().numpy(), y_ref, rtol=1.6e-2, atol=1.6e-2)
+    xr = torch.from_numpy((rng.standard_normal((40, 300)) * 2).astype(np.float32))
+    np.testing.assert_allclose(tr.logsumexp(xr).numpy(), orc.logsumexp(xr.numpy(), "float32"),
+                               rtol=1e-5, atol=1e-5)
+    assert np.array_equal(tr.argmax(xr).numpy(), orc.argreduce(xr.numpy(), -1))
+    q, k, v = (torch.from_numpy(rng.standard_normal((1, 48, 2, 64)).astype(np.float32)).bfloat16()
+               for _ in range(3))
+    for causal in (False, True):
+        o_ref, _ = orc.mha_fwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal,
+                               "bfloat16")
+        np.testing.assert_allclose(tr.mha_fwd(q, k, v, causal).float().numpy(), o_ref,
+                                   rtol=1e-2, atol=1e-2)
+
+
+def test_torch_gdn_sequential_matches_the_oracle():
+    from oracle import torch_ref as tr
+
+    rng = np.random.default_rng(22)
+    B, T, H, K, V = 1, 40, 2, 16, 8
+    q = rng.standard_normal((B, T, H, K)).astype(np.float32)
+    k = rng.standard_normal((B, T, H, K)).astype(np.float32)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((B, T, H, V)).astype(np.float32)
+    g = -np.abs(rng.standard_normal((B, T, H))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((B, T, H))))).astype(np.float32)
+    o, S = tr.gdn_sequential(*(torch.from_numpy(a) for a in (q, k, v, g, beta)), 0.25)
+    o_ref, S_ref = orc.gdn_sequential(q, k, v, g, beta, None, 0.25)
+    np.testing.assert_allclose(o.numpy(), o_ref, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(S.numpy(), S_ref, rtol=1e-4, atol=1e-5)
