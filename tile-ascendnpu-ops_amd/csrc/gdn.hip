@@ -28,9 +28,8 @@
 // four compute wavefronts keep the state slice in MFMA accumulators
 // (wavefront i owns key rows 32i..32i+31) and exchange its bf16 copy, U =
 // v - exp(gc) o (k S) and W through LDS; four loader wavefronts bring the
-// next chunk's k and record into LDS with direct-to-LDS loads meanwhile.
-// The output wavefronts read their q rows straight into registers.  Three
-// workgroup barriers per chunk.
+// next chunk's k, q, v slice and record into LDS with direct-to-LDS loads
+// meanwhile.  Three workgroup barriers per chunk.
 #include <algorithm>
 #include <mutex>
 
