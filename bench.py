@@ -387,8 +387,10 @@ def bench_suite(steps: int, warmup: int, only=None) -> dict:
             if not want(name, "MultiHeadAttentionFwdOp"):
                 continue
             op = MultiHeadAttentionFwdOp(B, H, S, D, causal, torch.bfloat16)
+            # at least 3 warm-up and 10 timed launches (~2 ms each): fewer
+            # are timed while the clocks are still settling
             k, v = _mfma_entry(name, op, [(q, kk, vv)], op.eval_roofline()[0],
-                               max(3, steps // 4), max(1, warmup // 2),
+                               max(10, steps // 2), max(3, warmup),
                                "bf16 q, k, v (8, 4096, 32, 128) BSHD, scale 1/sqrt(128)")
             out[k] = v
             _log(f"{k}: {v}")

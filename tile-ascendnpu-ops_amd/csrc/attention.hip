@@ -55,6 +55,7 @@ template <> struct Mfma<f16> {
 // more than 2^kLazyLog2 in the exp2 domain, so P <= 2^kLazyLog2 (exact in
 // fp32 / bf16) and the O accumulator is rescaled rarely.
 constexpr float kLazyLog2 = 8.0f;
+constexpr float kLazyBound = 256.0f;  // 2^kLazyLog2
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -90,9 +91,13 @@ __device__ __forceinline__ void lds_barrier() {
 // land at LDS byte address lds + 16 l.  Issued as inline assembly so that the
 // compiler does not track the LDS write: every wait for these loads is
 // explicit (vmcnt) and followed by a workgroup barrier before any wavefront
-// reads the data.
+// reads the data.  The compiler's hazard checks do not look into inline
+// assembly: the load starts with the one wait state the ISA requires after
+// the SALU write of M0 that precedes it (its base comes from SALU
+// arithmetic, so no VALU-to-SGPR wait is involved).
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(lds)
+               : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -113,37 +118,21 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
-// Per-lane source byte offsets of the tile gather: the four wavefronts of a
-// group take every fourth 1 KB window of a swizzled [BN][D] tile; lane l of
-// window `win` fills LDS chunk win * 64 + l, i.e. row r = (win * 64 + l) /
-// (D / 8), position p, with global chunk p ^ key(r) of key row min(r, rmax).
-template <typename T, int D, int BN, bool IS_V>
-__device__ __forceinline__ void gather_offsets(uint32_t (&off)[BN * D / 2048], int64_t stride,
-                                               int rmax, int gw, int lane) {
-  constexpr int CPR = D / 8;
-#pragma unroll
-  for (int i = 0; i < BN * D / 2048; ++i) {
-    const int win = 4 * i + gw;
-    const int ch = win * 64 + lane;
-    const int r = ch / CPR, p = ch % CPR;
-    const int key = IS_V ? Swz<D>::v_key(r) : Swz<D>::k_key(r);
-    off[i] = (uint32_t)(((int64_t)min(r, rmax) * stride + ((p ^ key) << 3)) * sizeof(T));
-  }
-}
-
 // Ping-pong schedule.  The 8 wavefronts form two groups, A = waves 0-3 and
 // B = waves 4-7, so that each SIMD hosts one wavefront of each.  A tile step
 // tau has two phases separated by workgroup barriers; in every phase one
 // group runs only MFMA work (O += V^T P^T of tile tau - 1, then S of tile
-// tau) while the other runs its softmax and issues direct-to-LDS loads:
-//   phase 0:  A: O(tau-1), S(tau)      B: softmax(tau-1), K(tau+2) -> slot
-//   phase 1:  A: softmax(tau), V(tau+1) -> slot      B: O(tau-1), S(tau)
-// K and V have three LDS slots each (tile t in slot t mod 3): within step tau
-// the groups read K(tau) and V(tau-1), the slots being filled held K(tau-1)
-// / V(tau-2), and every load has until the end of the next step to land
-// (each group ends its softmax phase waiting for everything but the windows
-// it just issued: vmcnt(4) for D = 128, vmcnt(2) for D = 64, vmcnt(0) when
-// it issued none).
+// tau) and issues the direct-to-LDS loads of a tile two steps ahead between
+// its MFMAs, while the other group runs its softmax:
+//   phase 0:  A: O(tau-1), S(tau), V(tau+1) -> slot     B: softmax(tau-1)
+//   phase 1:  A: softmax(tau)     B: O(tau-1), S(tau), K(tau+2) -> slot
+// K and V have three LDS slots each (tile t in slot t mod 3).  Numbering the
+// phases from 0, K(t) is read in phases 2t (A) and 2t + 1 (B) and issued in
+// phase 2t - 3, V(t) is read in phases 2t + 2 (A) and 2t + 3 (B) and issued
+// in phase 2t - 2: after the tile three back in the same slot was last read
+// (phases 2t - 5 and 2t - 3), and each group ends every MFMA phase waiting
+// for everything but the windows it just issued (vmcnt(WPW)), so a tile has
+// landed two phases before its first reader.
 // tanh(y) = 1 - 2 / (1 + e^{2y}), saturating to +-1 through the
 // exponential's overflow / underflow (no branch)
 __device__ __forceinline__ float tanh_sat(float y) {
@@ -183,14 +172,29 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // --- XCD-aware block order: workgroups are dealt round-robin to the 8
   // XCDs; regroup so that one XCD works through all query blocks of a head
-  // together and that head's K/V stays in the XCD's L2.
+  // together and that head's K/V stays in the XCD's L2.  Causal blocks
+  // differ in length: they go longest first over pairs of heads (the query
+  // blocks of two heads interleaved), so that the last workgroups an XCD
+  // receives are short ones.
   const int total = nqb * H * B;
   int id = blockIdx.x;
   if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
-  int qb = id % nqb;
-  const int hq = (id / nqb) % H;
-  const int bb = id / (nqb * H);
-  if (CAUSAL) qb = nqb - 1 - qb;  // longest rows first inside a head
+  int qb, head;
+  if (CAUSAL) {
+    const int pair = id / (2 * nqb), k2 = id - pair * 2 * nqb;
+    if (2 * pair + 1 < H * B) {
+      head = 2 * pair + (k2 & 1);
+      qb = nqb - 1 - (k2 >> 1);
+    } else {  // an odd last head on its own
+      head = 2 * pair;
+      qb = nqb - 1 - k2;
+    }
+  } else {
+    qb = id % nqb;
+    head = id / nqb;
+  }
+  const int hq = head % H;
+  const int bb = head / H;
   const int hk = hq / (H / Hkv);
   const int q0 = qb * BM;
   const int off = Skv - Sq;  // right-aligned causal offset
@@ -217,44 +221,40 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int kv_end = CAUSAL ? min(Skv, q0 + BM + off) : Skv;
   const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
-  // Gather offsets of this wavefront's windows (group B loads K, group A
-  // loads V); the last tile, if ragged, uses offsets with its rows clamped
-  // to the last key row (their scores are masked to -inf).  Tiles past the
-  // last one are not loaded, so every row index stays in [0, Skv).
+  // Direct-to-LDS tile loads (group B loads K, group A loads V).  Window i
+  // (of NW) of tile t: lane l fills LDS chunk (4 i + gw) * 64 + l of the
+  // tile's swizzled image, i.e. row r = i * WROWS + rl, position p = l mod
+  // (D / 8), with global chunk p ^ key(r) of key row min(r, rmax): rows past
+  // the last key repeat it (their scores are masked).  The swizzle key of a
+  // row depends only on rl, so the per-lane constants are rl and the chunk's
+  // byte offset.  A tile past the last one (the schedule issues its loads
+  // regardless) re-reads the last tile into its own slot, which no phase
+  // reads, so every load is in bounds and the wait counts never vary.
   constexpr int NW = BN * D / 2048;  // windows per wavefront per tile (== WPW)
   static_assert(NW == WPW, "window count");
-  uint32_t goff[NW];
-  if (grp_a)
-    gather_offsets<T, D, BN, true>(goff, kv_row, BN - 1, gw, lane);
-  else
-    gather_offsets<T, D, BN, false>(goff, kv_row, BN - 1, gw, lane);
+  constexpr int CPR = D / 8;         // 16-byte chunks per row
+  constexpr int WROWS = 256 / CPR;   // rows between a wavefront's windows
+  const int rl = gw * (64 / CPR) + lane / CPR;
+  const int rkey = grp_a ? Swz<D>::v_key(rl) : Swz<D>::k_key(rl);
+  const uint32_t cbyte = (uint32_t)((((lane % CPR) ^ rkey) << 3) * sizeof(T));
+  const uint32_t row_bytes = (uint32_t)(kv_row * sizeof(T));
   const T* gsrc = grp_a ? vbase : kbase;
   T* gdst = grp_a ? v_lds : k_lds;
-  auto load_tile = [&](int t) __device__ __attribute__((always_inline)) {
-    if (t >= ntiles) return;
-    const T* src = gsrc + (int64_t)t * BN * kv_row;
+  auto load_window = [&](int t, int i) __device__ __attribute__((always_inline)) {
+    const int te = min(t, ntiles - 1);
+    const T* src = gsrc + (int64_t)te * BN * kv_row;
+    const int rmax = min(BN - 1, Skv - 1 - te * BN);
     const uint32_t lds = lds_addr(gdst + (uint32_t)(t % 3) * TILE) + (uint32_t)gw * 1024;
-    if (t * BN + BN <= Skv) {
-#pragma unroll
-      for (int i = 0; i < NW; ++i) lds_dma16(src, goff[i], lds + i * 4096);
-    } else {
-      uint32_t c[NW];
-      if (grp_a)
-        gather_offsets<T, D, BN, true>(c, kv_row, Skv - 1 - t * BN, gw, lane);
-      else
-        gather_offsets<T, D, BN, false>(c, kv_row, Skv - 1 - t * BN, gw, lane);
-#pragma unroll
-      for (int i = 0; i < NW; ++i) lds_dma16(src, c[i], lds + i * 4096);
-    }
+    lds_dma16(src, (uint32_t)min(i * WROWS + rl, rmax) * row_bytes + cbyte, lds + i * 4096);
   };
-  // End of a softmax phase: every tile this wavefront loaded earlier has
-  // landed (the other group reads it after the next barrier); the WPW
-  // windows of tile t, issued in this phase if t exists, may stay in flight.
-  auto wait_loads = [&](int t) __device__ __attribute__((always_inline)) {
-    if (t < ntiles)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | WPW);  // vmcnt(WPW)
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  auto load_tile = [&](int t) __device__ __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) load_window(t, i);
+  };
+  // End of an MFMA phase: every tile this wavefront loaded earlier has
+  // landed; the WPW windows issued in this phase may stay in flight.
+  auto wait_loads = [&]() __device__ __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0F70 | WPW);  // vmcnt(WPW)
   };
 
   f32x16 acc_o[DBLK];
@@ -311,15 +311,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // The MFMA phase as one sequence: per 16-key step j, the DBLK O^T blocks
   // of keys 16 j .. 16 j + 15 (when DO_O), then the S^T products of head-dim
   // steps KS4 j .. KS4 j + KS4 - 1 for both 32-key blocks (when DO_S), so
-  // that up to DBLK + 2 independent accumulators alternate; each operand is
-  // read from LDS PF MFMAs ahead into a ring of PF + 1 register sets.
-  auto mfma_phase = [&](auto do_o, auto do_s, const T* vl, const T* kl)
+  // that up to DBLK + 2 independent accumulators alternate.  Each operand is
+  // read from LDS PF MFMAs ahead into a ring of PF + 1 register sets, and
+  // the order MFMA, then the reads of the operand PF ahead, is pinned with
+  // scheduling groups: left alone, the scheduler issues most reads just
+  // before their MFMA and waits out the LDS latency each time.  With LD,
+  // the NW windows of tile lt are issued one every N / NW MFMAs.
+  auto mfma_phase = [&](auto do_o, auto do_s, auto ld, const T* vl, const T* kl, int lt)
       __device__ __attribute__((always_inline)) {
     constexpr bool DO_O = decltype(do_o)::value, DO_S = decltype(do_s)::value;
+    constexpr bool LD = decltype(ld)::value;
     constexpr int KS4 = KSTEPS / 4;                        // head-dim steps per 16-key step
     constexpr int WO = DO_O ? DBLK : 0, WS = DO_S ? KS4 * NKB : 0;
     constexpr int W = WO + WS;                             // MFMAs per 16-key step
     constexpr int N = 4 * W;
+    constexpr int LDSTEP = N / NW, LDPOS = LDSTEP > 5 ? 5 : LDSTEP - 1;
     static_assert(BN / 16 == 4 && KSTEPS % 4 == 0, "four 16-key steps per tile");
     if (DO_S) {
 #pragma unroll
@@ -346,10 +352,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (w < WO) return read_vt(vb[w], j);
       return read_k(kb[KS4 * j + (w - WO) / NKB], (w - WO) % NKB);
     };
-    constexpr int PF = 3;  // operand reads in flight ahead of the MFMA using them
+    // LDS read instructions of operand n: two transpose reads for V^T, one
+    // 16-byte read for K (the scheduling-group sizes must be constants)
+    auto group_reads = [&](int n) __device__ __attribute__((always_inline)) {
+      if ((n % W) < WO) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    };
+    constexpr int PF = 4;  // operand reads in flight ahead of the MFMA using them
     V8 ring[PF + 1];
 #pragma unroll
     for (int n = 0; n < PF; ++n) ring[n] = fetch(n);
+#pragma unroll
+    for (int n = 0; n < PF; ++n) group_reads(n);
 #pragma unroll
     for (int n = 0; n < N; ++n) {
       if (n + PF < N) ring[(n + PF) % (PF + 1)] = fetch(n + PF);
@@ -360,10 +374,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int ks = KS4 * j + (w - WO) / NKB, kb = (w - WO) % NKB;
         acc_s[kb] = Mfma<T>::run(ring[n % (PF + 1)], qreg[ks], acc_s[kb]);
       }
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // this MFMA
+      if (n + PF < N) group_reads(n + PF);
+      if (LD && n % LDSTEP == LDPOS) load_window(lt, n / LDSTEP);
     }
   };
   typedef std::integral_constant<bool, true> yes;
   typedef std::integral_constant<bool, false> no;
+
+  // P = exp2(scale_log2 * s + neg_mc) of the tile in acc_s into pb (the
+  // MFMA operand, rounded to the storage type); returns this lane's partial
+  // row sum of the fp32 probabilities (the sum and the LSE stay in fp32).
+  auto exps = [&](float neg_mc) __device__ __attribute__((always_inline)) -> float {
+    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[kb][r], scale_log2, neg_mc));
+        ps[r & 3] += p;
+        pb[kb * 2 + (r >> 3)][r & 7] = (T)p;
+      }
+    }
+    return (ps[0] + ps[1]) + (ps[2] + ps[3]);
+  };
 
   // online softmax of tile t for query row qi: maxima in raw score units,
   // the scale (times log2 e) folded into one FMA per score inside exp2
@@ -389,18 +423,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
-    // four independent max / sum chains (fp32 max is exact in any order)
-    float tm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    // Exponentials against the running max first: while every P of the
+    // tile stays <= 2^kLazyLog2 (certain when this lane's partial sum does,
+    // all terms being >= 0) the running max need not move and the tile's
+    // max is never formed.  Otherwise (a new row max, a row without a
+    // reference max yet, a NaN) the wavefront forms the tile max, rescales
+    // and recomputes.  The two lanes of a row see the same max either way.
+    float ps = exps(m_run == -INFINITY ? 0.0f : -m_run * scale_log2);
+    if (__any(!(ps <= kLazyBound) || m_run == -INFINITY)) {
+      float tm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
+      for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], acc_s[kb][r]);
-    }
-    float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
-    tmax = pair_max(tmax);
-    const bool grow = tmax > m_run + lazy_raw;
-    if (__any(grow)) {
-      const float m_new = grow ? tmax : m_run;
+        for (int r = 0; r < 16; ++r) tm[r & 3] = fmaxf(tm[r & 3], acc_s[kb][r]);
+      }
+      const float tmax = pair_max(fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3])));
+      const float m_new = fmaxf(m_run, tmax);
       const float alpha = m_run == -INFINITY ? 0.0f
                                              : __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
       m_run = m_new;
@@ -410,22 +448,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[db][r] *= alpha;
       }
+      // rows with no visible key yet keep m = -inf: shift by 0 so exp2 -> 0
+      ps = exps(m_run == -INFINITY ? 0.0f : -m_run * scale_log2);
     }
-    // rows with no visible key yet keep m = -inf: shift by 0 so exp2 -> 0
-    const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * scale_log2;
-    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        // fp32 probabilities form the row sum (and the LSE); P is rounded to
-        // the storage type only as the MFMA operand
-        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[kb][r], scale_log2, neg_mc));
-        ps[r & 3] += p;
-        pb[kb * 2 + (r >> 3)][r & 7] = (T)p;
-      }
-    }
-    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    l_run += ps;
     // materialise P here: pure arithmetic may otherwise sink past the next
     // barrier into the O update, out of the phase meant to overlap the
     // other group's MFMA work
@@ -435,57 +461,63 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
 
   // --- prologue: K(0), K(1) (group B) and V(0) (group A) into their slots
-  load_tile(0);
-  if (!grp_a) load_tile(1);
+  if (ntiles > 0) {
+    load_tile(0);
+    if (!grp_a) load_tile(1);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   // One loop per group, each body a softmax phase then an MFMA phase (group
   // A's steps rotated by half a step so that both loops have that shape);
-  // both pass 2 (ntiles + 1) barriers in all.
-  //   A, tau:  softmax(tau), V(tau+1) | O(tau), S(tau+1)
-  //   B, tau:  softmax(tau-1), K(tau+2) | O(tau-1), S(tau)
-  // The last step of each loop (O only, no S) is peeled off, so that the
-  // loop body holds a single MFMA sequence.
+  // both pass 2 (ntiles + 1) barriers in all.  With phases numbered from 0:
+  //   A: phase 0: S(0), V(1);  then per tau: softmax(tau) | O(tau), S(tau+1), V(tau+2)
+  //   B: phase 1: S(0), K(2);  then per tau: softmax(tau-1) | O(tau-1), S(tau), K(tau+2)
+  // The last step of each loop (O only, no S, no loads) is peeled off, so
+  // that the loop body holds a single MFMA sequence.
   if (grp_a) {
-    if (ntiles > 0) mfma_phase(no(), yes(), v_lds, k_lds);  // S(0)
+    if (ntiles > 0) {
+      mfma_phase(no(), yes(), yes(), v_lds, k_lds, 1);
+      wait_loads();
+    }
     lds_barrier();
     for (int tau = 0; tau + 1 < ntiles; ++tau) {
-      load_tile(tau + 1);
       softmax(tau);
-      wait_loads(tau + 1);
       lds_barrier();
-      mfma_phase(yes(), yes(), v_lds + (tau % 3) * TILE, k_lds + ((tau + 1) % 3) * TILE);
+      mfma_phase(yes(), yes(), yes(), v_lds + (tau % 3) * TILE, k_lds + ((tau + 1) % 3) * TILE,
+                 tau + 2);
+      wait_loads();
       lds_barrier();
     }
     if (ntiles > 0) {
       const int tau = ntiles - 1;
       softmax(tau);
-      wait_loads(ntiles);
       lds_barrier();
-      mfma_phase(yes(), no(), v_lds + (tau % 3) * TILE, k_lds);
+      mfma_phase(yes(), no(), no(), v_lds + (tau % 3) * TILE, k_lds, -1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
     }
     lds_barrier();  // softmax phase of step ntiles (nothing left to do)
   } else {
-    load_tile(2);
-    wait_loads(2);
-    lds_barrier();
-    if (ntiles > 0) mfma_phase(no(), yes(), v_lds, k_lds);  // S(0)
+    lds_barrier();  // phase 0: group A computes S(0)
+    if (ntiles > 0) {
+      mfma_phase(no(), yes(), yes(), v_lds, k_lds, 2);
+      wait_loads();
+    }
     lds_barrier();
     for (int tau = 1; tau < ntiles; ++tau) {
-      load_tile(tau + 2);
       softmax(tau - 1);
-      wait_loads(tau + 2);
       lds_barrier();
-      mfma_phase(yes(), yes(), v_lds + ((tau - 1) % 3) * TILE, k_lds + (tau % 3) * TILE);
+      mfma_phase(yes(), yes(), yes(), v_lds + ((tau - 1) % 3) * TILE, k_lds + (tau % 3) * TILE,
+                 tau + 2);
+      wait_loads();
       lds_barrier();
     }
     if (ntiles > 0) {
       const int tau = ntiles;
       softmax(tau - 1);
-      wait_loads(ntiles);
       lds_barrier();
-      mfma_phase(yes(), no(), v_lds + ((tau - 1) % 3) * TILE, k_lds);
+      mfma_phase(yes(), no(), no(), v_lds + ((tau - 1) % 3) * TILE, k_lds, -1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
     }
   }
