@@ -288,11 +288,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     voff[db] = vrow * D + ((((dim >> 3) ^ Swz<D>::v_key(vrow)) << 3) | (dim & 7));
   }
 
-  // Operand reads: `vb` / `kb` are the LDS byte addresses of this lane's
-  // first V^T / K element in the current slots, re-derived at the start of
-  // each MFMA phase and made opaque, so that the per-read constants (key
-  // and head-dim steps) become DS immediate offsets rather than one address
-  // computation per read.
+  // Operand reads: `vb0` / `kb0` are the LDS byte addresses of this lane's
+  // first V^T / K element in slot 0, made opaque once, so that the
+  // per-read constants (slot, key and head-dim steps) become DS immediate
+  // offsets rather than one address computation per read.
+  uint32_t vb0[DBLK], kb0[KSTEPS];
+#pragma unroll
+  for (int db = 0; db < DBLK; ++db) {
+    vb0[db] = lds_addr(v_lds) + voff[db] * (uint32_t)sizeof(T);
+    asm volatile("" : "+v"(vb0[db]));
+  }
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    kb0[ks] = lds_addr(k_lds) + koff[ks] * (uint32_t)sizeof(T);
+    asm volatile("" : "+v"(kb0[ks]));
+  }
   typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
   typedef __attribute__((address_space(3))) V8 lds_v8;
   // A operand of the O^T update: 8 keys (16 ks + 8 rr + ..) of dim block db,
@@ -317,7 +327,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // scheduling groups: left alone, the scheduler issues most reads just
   // before their MFMA and waits out the LDS latency each time.  With LD,
   // the NW windows of tile lt are issued one every N / NW MFMAs.
-  auto mfma_phase = [&](auto do_o, auto do_s, auto ld, const T* vl, const T* kl, int lt)
+  auto mfma_phase = [&](auto do_o, auto do_s, auto ld, auto vslot, auto kslot, int lt)
       __device__ __attribute__((always_inline)) {
     constexpr bool DO_O = decltype(do_o)::value, DO_S = decltype(do_s)::value;
     constexpr bool LD = decltype(ld)::value;
@@ -331,22 +341,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) acc_s[kb] = f32x16{};
     }
+    // slot offsets: immediate DS offsets when the slot is a compile-time
+    // constant (the unrolled loop), one add per address otherwise
     uint32_t vb[DBLK], kb[KSTEPS];
-    const uint32_t vl_addr = lds_addr(vl), kl_addr = lds_addr(kl);
-    if (DO_O) {
+    const uint32_t vso = (uint32_t)(int)vslot * TILE * (uint32_t)sizeof(T);
+    const uint32_t kso = (uint32_t)(int)kslot * TILE * (uint32_t)sizeof(T);
 #pragma unroll
-      for (int db = 0; db < DBLK; ++db) {
-        vb[db] = vl_addr + voff[db] * 2;
-        asm volatile("" : "+v"(vb[db]));
-      }
-    }
-    if (DO_S) {
+    for (int db = 0; db < DBLK; ++db) vb[db] = vb0[db] + vso;
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        kb[ks] = kl_addr + koff[ks] * 2;
-        asm volatile("" : "+v"(kb[ks]));
-      }
-    }
+    for (int ks = 0; ks < KSTEPS; ++ks) kb[ks] = kb0[ks] + kso;
     auto fetch = [&](int n) __device__ __attribute__((always_inline)) -> V8 {
       const int j = n / W, w = n % W;
       if (w < WO) return read_vt(vb[w], j);
@@ -472,27 +475,43 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // both pass 2 (ntiles + 1) barriers in all.  With phases numbered from 0:
   //   A: phase 0: S(0), V(1);  then per tau: softmax(tau) | O(tau), S(tau+1), V(tau+2)
   //   B: phase 1: S(0), K(2);  then per tau: softmax(tau-1) | O(tau-1), S(tau), K(tau+2)
-  // The last step of each loop (O only, no S, no loads) is peeled off, so
-  // that the loop body holds a single MFMA sequence.
+  // The last step of each loop (O only, no S, no loads) is peeled off, and
+  // the loops are unrolled by three so that every slot index is a constant
+  // (tile t lives in slot t mod 3).
+  typedef std::integral_constant<int, 0> s0;
+  typedef std::integral_constant<int, 1> s1;
+  typedef std::integral_constant<int, 2> s2;
+  // one loop step: softmax phase, then MFMA phase (slots as constants)
+  auto step = [&](auto vslot, auto kslot, int t_soft, int t_load) __device__ __attribute__((always_inline)) {
+    softmax(t_soft);
+    lds_barrier();
+    mfma_phase(yes(), yes(), yes(), vslot, kslot, t_load);
+    wait_loads();
+    lds_barrier();
+  };
   if (grp_a) {
     if (ntiles > 0) {
-      mfma_phase(no(), yes(), yes(), v_lds, k_lds, 1);
+      mfma_phase(no(), yes(), yes(), s0(), s0(), 1);
       wait_loads();
     }
     lds_barrier();
-    for (int tau = 0; tau + 1 < ntiles; ++tau) {
-      softmax(tau);
-      lds_barrier();
-      mfma_phase(yes(), yes(), yes(), v_lds + (tau % 3) * TILE, k_lds + ((tau + 1) % 3) * TILE,
-                 tau + 2);
-      wait_loads();
-      lds_barrier();
+    // step tau: softmax(tau) | O(tau) (V slot tau % 3), S(tau + 1) (K slot (tau + 1) % 3)
+    int tau = 0;
+    for (; tau + 3 < ntiles; tau += 3) {
+      step(s0(), s1(), tau, tau + 2);
+      step(s1(), s2(), tau + 1, tau + 3);
+      step(s2(), s0(), tau + 2, tau + 4);
+    }
+    if (tau + 1 < ntiles) {
+      step(s0(), s1(), tau, tau + 2);
+      ++tau;
+      if (tau + 1 < ntiles) step(s1(), s2(), tau, tau + 2);
     }
     if (ntiles > 0) {
-      const int tau = ntiles - 1;
-      softmax(tau);
+      const int t = ntiles - 1;
+      softmax(t);
       lds_barrier();
-      mfma_phase(yes(), no(), no(), v_lds + (tau % 3) * TILE, k_lds, -1);
+      mfma_phase(yes(), no(), no(), t % 3, 0, -1);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
     }
@@ -500,23 +519,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   } else {
     lds_barrier();  // phase 0: group A computes S(0)
     if (ntiles > 0) {
-      mfma_phase(no(), yes(), yes(), v_lds, k_lds, 2);
+      mfma_phase(no(), yes(), yes(), s0(), s0(), 2);
       wait_loads();
     }
     lds_barrier();
-    for (int tau = 1; tau < ntiles; ++tau) {
-      softmax(tau - 1);
-      lds_barrier();
-      mfma_phase(yes(), yes(), yes(), v_lds + ((tau - 1) % 3) * TILE, k_lds + (tau % 3) * TILE,
-                 tau + 2);
-      wait_loads();
-      lds_barrier();
+    // step tau: softmax(tau - 1) | O(tau - 1) (V slot (tau - 1) % 3), S(tau) (K slot tau % 3)
+    int tau = 1;
+    for (; tau + 2 < ntiles; tau += 3) {
+      step(s0(), s1(), tau - 1, tau + 2);
+      step(s1(), s2(), tau, tau + 3);
+      step(s2(), s0(), tau + 1, tau + 4);
+    }
+    if (tau < ntiles) {
+      step(s0(), s1(), tau - 1, tau + 2);
+      ++tau;
+      if (tau < ntiles) step(s1(), s2(), tau - 1, tau + 2);
     }
     if (ntiles > 0) {
-      const int tau = ntiles;
-      softmax(tau - 1);
+      const int t = ntiles;
+      softmax(t - 1);
       lds_barrier();
-      mfma_phase(yes(), no(), no(), v_lds + ((tau - 1) % 3) * TILE, k_lds, -1);
+      mfma_phase(yes(), no(), no(), (t - 1) % 3, 0, -1);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
     }
