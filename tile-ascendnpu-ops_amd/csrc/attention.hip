@@ -2,8 +2,10 @@
 //
 // One workgroup = 8 wavefronts = BM = 256 query rows of one (batch, head);
 // each wavefront owns 32 query rows.  Keys/values stream through LDS in
-// tiles of BN = 64 rows, three LDS slots per operand, filled by
-// direct-to-LDS loads (no register staging) two tile steps ahead.
+// tiles of BN rows filled by direct-to-LDS loads (no register staging):
+// BN = 128 with two LDS slots per operand for D = 128 (128 KB), BN = 64
+// with three slots for D = 64.  The longer tile halves the barriers and
+// per-tile bookkeeping per key.
 //
 // Both products run on v_mfma_f32_32x32x16_{bf16,f16} in the *transposed*
 // orientation:
@@ -122,10 +124,12 @@ __device__ __forceinline__ float pair_sum(float x) {
 // B = waves 4-7, so that each SIMD hosts one wavefront of each.  A tile step
 // tau has two phases separated by workgroup barriers; in every phase one
 // group runs only MFMA work (O += V^T P^T of tile tau - 1, then S of tile
-// tau) and issues the direct-to-LDS loads of a tile two steps ahead between
-// its MFMAs, while the other group runs its softmax:
+// tau) while the other runs its softmax.  With three slots (BN = 64) the
+// MFMA group also issues the direct-to-LDS loads of a tile two steps ahead
+// between its MFMAs:
 //   phase 0:  A: O(tau-1), S(tau), V(tau+1) -> slot     B: softmax(tau-1)
 //   phase 1:  A: softmax(tau)     B: O(tau-1), S(tau), K(tau+2) -> slot
+// (the two-slot schedule of BN = 128 is described at the loops).
 // K and V have three LDS slots each (tile t in slot t mod 3).  Numbering the
 // phases from 0, K(t) is read in phases 2t (A) and 2t + 1 (B) and issued in
 // phase 2t - 3, V(t) is read in phases 2t + 2 (A) and 2t + 3 (B) and issued
@@ -156,11 +160,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int DBLK = D / 32;    // 32-row blocks of O^T
   constexpr int TILE = BN * D;    // elements per K or V tile
   constexpr int WPW = TILE / 512 / 4;  // 1 KB load windows per wavefront per tile
-  static_assert(BN == 64, "the schedule assumes 64-key tiles");
+  static_assert(BN == 64 || (BN == 128 && D == 128), "tile shapes");
   static_assert(WPW >= 1 && WPW <= 15, "vmcnt immediate");
+  constexpr int NSLOT = BN == 64 ? 3 : 2;  // LDS slots per operand
 
-  __shared__ __attribute__((aligned(16))) T k_lds[3 * TILE];
-  __shared__ __attribute__((aligned(16))) T v_lds[3 * TILE];
+  __shared__ __attribute__((aligned(16))) T k_lds[NSLOT * TILE];
+  __shared__ __attribute__((aligned(16))) T v_lds[NSLOT * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -244,7 +249,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int te = min(t, ntiles - 1);
     const T* src = gsrc + (int64_t)te * BN * kv_row;
     const int rmax = min(BN - 1, Skv - 1 - te * BN);
-    const uint32_t lds = lds_addr(gdst + (uint32_t)(t % 3) * TILE) + (uint32_t)gw * 1024;
+    const uint32_t lds = lds_addr(gdst + (uint32_t)(t % NSLOT) * TILE) + (uint32_t)gw * 1024;
     lds_dma16(src, (uint32_t)min(i * WROWS + rl, rmax) * row_bytes + cbyte, lds + i * 4096);
   };
   auto load_tile = [&](int t) __device__ __attribute__((always_inline)) {
@@ -331,12 +336,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       __device__ __attribute__((always_inline)) {
     constexpr bool DO_O = decltype(do_o)::value, DO_S = decltype(do_s)::value;
     constexpr bool LD = decltype(ld)::value;
-    constexpr int KS4 = KSTEPS / 4;                        // head-dim steps per 16-key step
+    constexpr int J = BN / 16;                             // 16-key steps per tile
+    constexpr int KS4 = KSTEPS / J;                        // head-dim steps per 16-key step
     constexpr int WO = DO_O ? DBLK : 0, WS = DO_S ? KS4 * NKB : 0;
     constexpr int W = WO + WS;                             // MFMAs per 16-key step
-    constexpr int N = 4 * W;
+    constexpr int N = J * W;
     constexpr int LDSTEP = N / NW, LDPOS = LDSTEP > 5 ? 5 : LDSTEP - 1;
-    static_assert(BN / 16 == 4 && KSTEPS % 4 == 0, "four 16-key steps per tile");
+    static_assert(KSTEPS % J == 0, "head-dim steps per 16-key step");
     if (DO_S) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) acc_s[kb] = f32x16{};
@@ -481,6 +487,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   typedef std::integral_constant<int, 0> s0;
   typedef std::integral_constant<int, 1> s1;
   typedef std::integral_constant<int, 2> s2;
+  if constexpr (NSLOT == 3) {
   // one loop step: softmax phase, then MFMA phase (slots as constants)
   auto step = [&](auto vslot, auto kslot, int t_soft, int t_load) __device__ __attribute__((always_inline)) {
     softmax(t_soft);
@@ -544,6 +551,73 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lds_barrier();
     }
   }
+  } else {
+  // Two slots (128-key tiles).  K(t) is read in phases 2t (A) and 2t + 1
+  // (B); group B issues it in its softmax phase 2t - 2 and waits for it at
+  // the end of phase 2t - 1.  V(t) is read in phases 2t + 2 (A) and 2t + 3
+  // (B); group A issues it between the MFMAs of phase 2t and waits for it
+  // at the end of phase 2t + 1.  Either way the slot's previous tile (t - 2)
+  // was last read in the phase before the issue.
+  if (grp_a) {
+    if (ntiles > 0) mfma_phase(no(), yes(), no(), s0(), s0(), -1);  // phase 0: S(0)
+    lds_barrier();
+    // step tau: softmax(tau) | O(tau) (V slot tau % 2), S(tau + 1), V(tau + 1)
+    auto step_a = [&](auto vslot, auto kslot, int tau) __device__ __attribute__((always_inline)) {
+      softmax(tau);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): V(tau) has landed
+      lds_barrier();
+      mfma_phase(yes(), yes(), yes(), vslot, kslot, tau + 1);
+      lds_barrier();
+    };
+    int tau = 0;
+    for (; tau + 2 < ntiles; tau += 2) {
+      step_a(s0(), s1(), tau);
+      step_a(s1(), s0(), tau + 1);
+    }
+    if (tau + 1 < ntiles) {
+      step_a(s0(), s1(), tau);
+      ++tau;
+    }
+    if (ntiles > 0) {
+      const int t = ntiles - 1;
+      softmax(t);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      lds_barrier();
+      mfma_phase(yes(), no(), no(), t % 2, 0, -1);
+      lds_barrier();
+    }
+    lds_barrier();  // softmax phase of step ntiles (nothing left to do)
+  } else {
+    lds_barrier();  // phase 0: group A computes S(0)
+    if (ntiles > 0) mfma_phase(no(), yes(), no(), s0(), s0(), -1);  // phase 1: S(0)
+    lds_barrier();
+    // step tau: softmax(tau - 1), K(tau + 1) | O(tau - 1) (V slot (tau - 1) % 2), S(tau)
+    auto step_b = [&](auto vslot, auto kslot, int tau) __device__ __attribute__((always_inline)) {
+      load_tile(tau + 1);
+      softmax(tau - 1);
+      lds_barrier();
+      mfma_phase(yes(), yes(), no(), vslot, kslot, -1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K(tau + 1) has landed
+      lds_barrier();
+    };
+    int tau = 1;
+    for (; tau + 1 < ntiles; tau += 2) {
+      step_b(s0(), s1(), tau);
+      step_b(s1(), s0(), tau + 1);
+    }
+    if (tau < ntiles) {
+      step_b(s0(), s1(), tau);
+      ++tau;
+    }
+    if (ntiles > 0) {
+      const int t = ntiles;
+      softmax(t - 1);
+      lds_barrier();
+      mfma_phase(yes(), no(), no(), (t - 1) % 2, 0, -1);
+      lds_barrier();
+    }
+  }
+  }
   __builtin_amdgcn_s_waitcnt(0);  // no load may land after the workgroup's LDS is released
 
   // --- epilogue: combine the two half-row sums, normalise, store
@@ -592,10 +666,10 @@ static int launch_w(const void* q, const void* k, const void* v, void* o, float*
                     hipStream_t s) {
   constexpr float kLog2e = 1.4426950408889634f;
   if (softcap > 0.0f)
-    launch_k<T, D, 64, true>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, 1.0f, scale / softcap,
+    launch_k<T, D, (D == 128 ? 128 : 64), true>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, 1.0f, scale / softcap,
                              softcap * kLog2e, s);
   else
-    launch_k<T, D, 64, false>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale * kLog2e, 0.0f,
+    launch_k<T, D, (D == 128 ? 128 : 64), false>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale * kLog2e, 0.0f,
                               0.0f, s);
   return launch_status();
 }
