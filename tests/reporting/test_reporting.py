@@ -301,3 +301,37 @@ def test_rocprof_script_rebuilds_op():
 def test_rocprof_rejects_closures():
     with pytest.raises(TypeError, match="events mode"):
         rp.bench_kernel_rocprof(lambda x: x, (torch.zeros(1),))
+
+
+def test_analyzer_attributes_cases_of_shared_test_files():
+    """Cases of a test file that several ops share go to the op whose class
+    name is in the case id, else the one whose test_keyword matches."""
+    catalog = [
+        {"name": "AddFwdOp", "test": "tests/ops/test_add_sub.py"},
+        {"name": "SubFwdOp", "test": "tests/ops/test_add_sub.py"},
+        {"name": "LerpFwdOp", "test": "tests/ops/test_lerp.py", "test_keyword": "lerp_scalar"},
+        {"name": "LerpTensorFwdOp", "test": "tests/ops/test_lerp.py", "test_keyword": "lerp_tensor"},
+    ]
+    case = lambda cls, name: {"classname": cls, "name": name}  # noqa: E731
+    pick = lambda c: analyzer._case_operator(c, catalog, None)  # noqa: E731
+    assert pick(case("tests.ops.test_add_sub", "test_add_sub[1-dtype0-shapes0-SubFwdOp--1.0]")) == "SubFwdOp"
+    assert pick(case("tests.ops.test_add_sub", "test_add_sub[1-dtype0-shapes0-AddFwdOp-1.0]")) == "AddFwdOp"
+    assert pick(case("tests.ops.test_lerp", "test_lerp_scalar_weights[0.3-dtype1]")) == "LerpFwdOp"
+    assert pick(case("tests.ops.test_lerp", "test_lerp_tensor[shapes0-dtype0]")) == "LerpTensorFwdOp"
+    assert pick(case("tests.ops.test_lerp", "test_lerp_dtype_mismatch_rejected")) is None
+
+
+def test_setup_gpu_label_from_gpu_agents(monkeypatch):
+    """The GPU label comes from rocminfo's GPU agent, not the CPU agent."""
+    from tileops.reporting import setup_info
+
+    out = ("*******\nAgent 1\n*******\n  Name:                    AMD EPYC 9575F\n"
+           "  Marketing Name:          AMD EPYC 9575F\n  Device Type:             CPU\n"
+           "*******\nAgent 2\n*******\n  Name:                    gfx950\n"
+           "  Marketing Name:          AMD Instinct MI355X\n  Device Type:             GPU\n")
+
+    class _Res:
+        stdout = out
+
+    monkeypatch.setattr(setup_info.subprocess, "run", lambda *a, **k: _Res())
+    assert setup_info._gpu_info() == "AMD Instinct MI355X (gfx950) x 1"

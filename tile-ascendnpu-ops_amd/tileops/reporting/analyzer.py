@@ -92,16 +92,35 @@ def _test_key(path: str | None) -> str:
     return PurePosixPath(path.replace("\\", "/")).stem.lower() if path else ""
 
 
+def _keyword_match(expr: str, hay: str) -> bool:
+    """A manifest ``test_keyword`` (pytest ``-k`` terms joined by ``or``)
+    against a lower-cased case name."""
+    terms = [t.strip().lower() for t in str(expr).split(" or ") if t.strip()]
+    return any(t in hay for t in terms)
+
+
 def _case_operator(case: dict[str, Any], catalog: list[dict[str, Any]],
                    default: str | None) -> str | None:
     """The op a JUnit case belongs to: its ``op`` property, else the one
-    manifest op whose test file names it, else ``default``."""
+    manifest op whose test file names it; when several ops share that file,
+    the one whose class name appears in the case id, else the one whose
+    ``test_keyword`` matches it; else ``default``."""
     declared = (case.get("properties") or {}).get("op")
     if declared:
         return str(declared)
-    hay = f"{case.get('classname', '')} {case.get('nodeid', '')}".lower()
-    hits = [e.get("name") for e in catalog if _test_key(e.get("test")) and _test_key(e.get("test")) in hay]
-    return hits[0] if len(set(hits)) == 1 else default
+    hay = f"{case.get('classname', '')} {case.get('nodeid', '')} {case.get('name', '')}".lower()
+    hits = [e for e in catalog if _test_key(e.get("test")) and _test_key(e.get("test")) in hay]
+    names = {e.get("name") for e in hits}
+    if len(names) == 1:
+        return hits[0].get("name")
+    if len(names) > 1:
+        by_class = {n for n in names if n and n.lower() in hay}
+        if len(by_class) == 1:
+            return by_class.pop()
+        by_kw = {e.get("name") for e in hits if e.get("test_keyword") and _keyword_match(e["test_keyword"], hay)}
+        if len(by_kw) == 1:
+            return by_kw.pop()
+    return default
 
 
 def _num_prop(case: dict[str, Any], name: str) -> float | None:

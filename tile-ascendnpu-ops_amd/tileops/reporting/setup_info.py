@@ -43,13 +43,18 @@ def _gpu_info() -> str | None:
                              check=False).stdout
     except (OSError, subprocess.SubprocessError):
         return None
-    names = re.findall(r"Marketing Name:\s*(.+)", out)
-    archs = re.findall(r"Name:\s*(gfx\w+)", out)
-    gpus = [n.strip() for n in names if "CPU" not in n and n.strip()]
-    if not archs:
+    # one block per agent; the GPU agents carry "Device Type: GPU"
+    gpus = []
+    for block in re.split(r"\n\*+\s*\n\s*Agent \d+", out):
+        if not re.search(r"Device Type:\s*GPU", block):
+            continue
+        arch = re.search(r"Name:\s*(gfx\w+)", block)
+        name = re.search(r"Marketing Name:\s*(.+)", block)
+        if arch:
+            gpus.append(((name.group(1).strip() if name else "") or "AMD GPU", arch.group(1)))
+    if not gpus:
         return None
-    label = gpus[0] if gpus else "AMD GPU"
-    return f"{label} ({archs[0]}) x {len(archs)}"
+    return f"{gpus[0][0]} ({gpus[0][1]}) x {len(gpus)}"
 
 
 def _cpu_info() -> str:
