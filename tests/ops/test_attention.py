@@ -123,6 +123,25 @@ def test_gqa_prefill_softcap(causal, softcap, dtype, D, sq, skv):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype, B, H, Hkv, sq, skv", [
+    (torch.bfloat16, 2, 4, 4, 512, 512),
+    (torch.float16, 1, 4, 2, 300, 437),    # grouped heads, ragged, right-aligned causal
+    (torch.bfloat16, 1, 2, 1, 64, 1100),   # one query block, many key tiles
+])
+def test_mha_head_dim_256(causal, dtype, B, H, Hkv, sq, skv):
+    # head dim 256 (the reference sizes its tiles for dim > 128,
+    # kernels/attention/multi_head_attention/multi_head_attention.py:251):
+    # two workgroups per query block, 128 output columns each
+    D = 256
+    q = torch.randn(B, sq, H, D, device="cuda", dtype=dtype)
+    k = torch.randn(B, skv, Hkv, D, device="cuda", dtype=dtype)
+    v = torch.randn(B, skv, Hkv, D, device="cuda", dtype=dtype)
+    o, lse = GQAPrefillFwdKernel(B, H, Hkv, sq, skv, D, causal, dtype)(q, k, v)
+    _check(q, k, v, o, lse, causal)
+
+
+@pytest.mark.gpu
 def test_mha_peaked_attention():
     # one key per query dominates: exercises large score ranges and rescaling
     B, S, H, D = 1, 256, 2, 64

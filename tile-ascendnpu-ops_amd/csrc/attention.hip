@@ -70,7 +70,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // cover all 64 banks once.
 template <int D> struct Swz {
   static constexpr int CPR = D / 8;  // chunks per row
-  __device__ __forceinline__ static int k_key(int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); }
+  __device__ __forceinline__ static int k_key(int r) { return CPR >= 16 ? (r & 15) : ((r >> 1) & 7); }
   __device__ __forceinline__ static int v_key(int r) { return CPR == 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 };
 
@@ -148,7 +148,10 @@ __device__ __forceinline__ float tanh_sat(float y) {
 // reference's order: scale, cap, then the causal mask), and carried in log2
 // units from the start of the softmax: the caller passes scale_log2 = 1,
 // cap_scale = scale / softcap and cap_log2 = softcap * log2 e.
-template <typename T, int D, bool CAUSAL, int BN, bool SOFTCAP>
+// D: the head dim of q, k and v rows; DV: the v columns (and output columns)
+// a workgroup computes, D itself up to 128, half of it for D = 256 (two
+// workgroups per query block, each forming the full scores).
+template <typename T, int D, int DV, bool CAUSAL, int BN, bool SOFTCAP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void mha_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
     float* __restrict__ lse, int B, int Sq, int Skv, int H, int Hkv, float scale_log2, int nqb,
@@ -157,15 +160,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int NKB = BN / 32;    // 32-key blocks per tile
   constexpr int BM = 256;         // query rows per workgroup (8 x 32)
   constexpr int KSTEPS = D / 16;  // MFMA steps over the head dim
-  constexpr int DBLK = D / 32;    // 32-row blocks of O^T
-  constexpr int TILE = BN * D;    // elements per K or V tile
-  constexpr int WPW = TILE / 512 / 4;  // 1 KB load windows per wavefront per tile
+  constexpr int DBLK = DV / 32;   // 32-row blocks of O^T
+  constexpr int TILE_K = BN * D;  // elements per K tile
+  constexpr int TILE_V = BN * DV; // elements per V tile (this workgroup's columns)
+  constexpr int NW_K = TILE_K / 2048, NW_V = TILE_V / 2048;  // 1 KB windows per wavefront
   static_assert(BN == 64 || (BN == 128 && D == 128), "tile shapes");
-  static_assert(WPW >= 1 && WPW <= 15, "vmcnt immediate");
+  static_assert(DV == D || (D == 256 && DV == 128), "value split");
+  static_assert(NW_V >= 1 && NW_K <= 15, "vmcnt immediate");
   constexpr int NSLOT = BN == 64 ? 3 : 2;  // LDS slots per operand
 
-  __shared__ __attribute__((aligned(16))) T k_lds[NSLOT * TILE];
-  __shared__ __attribute__((aligned(16))) T v_lds[NSLOT * TILE];
+  __shared__ __attribute__((aligned(16))) T k_lds[NSLOT * TILE_K];
+  __shared__ __attribute__((aligned(16))) T v_lds[NSLOT * TILE_V];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -181,9 +186,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // differ in length: they go longest first over pairs of heads (the query
   // blocks of two heads interleaved), so that the last workgroups an XCD
   // receives are short ones.
-  const int total = nqb * H * B;
+  // (the value halves of one query block, D = 256, are neighbours)
+  constexpr int NDV = D / DV;
+  const int nblk = (int)gridDim.x;
   int id = blockIdx.x;
-  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+  if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+  const int dv0 = (id % NDV) * DV;
+  id /= NDV;
   int qb, head;
   if (CAUSAL) {
     const int pair = id / (2 * nqb), k2 = id - pair * 2 * nqb;
@@ -208,7 +217,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int64_t kv_row = (int64_t)Hkv * D;
   const T* qbase = q + (int64_t)bb * Sq * q_row + (int64_t)hq * D;
   const T* kbase = k + (int64_t)bb * Skv * kv_row + (int64_t)hk * D;
-  const T* vbase = v + (int64_t)bb * Skv * kv_row + (int64_t)hk * D;
+  const T* vbase = v + (int64_t)bb * Skv * kv_row + (int64_t)hk * D + dv0;
 
   // --- Q^T operand: this lane's query row, 8 dims per MFMA step
   const int qi = q0 + wave * 32 + col;
@@ -229,37 +238,51 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Direct-to-LDS tile loads (group B loads K, group A loads V).  Window i
   // (of NW) of tile t: lane l fills LDS chunk (4 i + gw) * 64 + l of the
   // tile's swizzled image, i.e. row r = i * WROWS + rl, position p = l mod
-  // (D / 8), with global chunk p ^ key(r) of key row min(r, rmax): rows past
-  // the last key repeat it (their scores are masked).  The swizzle key of a
-  // row depends only on rl, so the per-lane constants are rl and the chunk's
-  // byte offset.  A tile past the last one (the schedule issues its loads
-  // regardless) re-reads the last tile into its own slot, which no phase
-  // reads, so every load is in bounds and the wait counts never vary.
-  constexpr int NW = BN * D / 2048;  // windows per wavefront per tile (== WPW)
-  static_assert(NW == WPW, "window count");
-  constexpr int CPR = D / 8;         // 16-byte chunks per row
-  constexpr int WROWS = 256 / CPR;   // rows between a wavefront's windows
-  const int rl = gw * (64 / CPR) + lane / CPR;
-  const int rkey = grp_a ? Swz<D>::v_key(rl) : Swz<D>::k_key(rl);
-  const uint32_t cbyte = (uint32_t)((((lane % CPR) ^ rkey) << 3) * sizeof(T));
+  // CPR (the row's 16-byte chunks), with global chunk p ^ key(r) of key row
+  // min(r, rmax): rows past the last key repeat it (their scores are
+  // masked).  When WROWS is a multiple of the swizzle key's period (16 rows)
+  // the key depends only on rl and the chunk's byte offset is one per-lane
+  // constant; with 512-byte rows (D = 256, WROWS = 8) it is formed per
+  // window.  A tile past the last one
+  // (the schedule issues its loads regardless) re-reads the last tile into
+  // its own slot, which no phase reads, so every load is in bounds and the
+  // wait counts never vary.
   const uint32_t row_bytes = (uint32_t)(kv_row * sizeof(T));
-  const T* gsrc = grp_a ? vbase : kbase;
-  T* gdst = grp_a ? v_lds : k_lds;
-  auto load_window = [&](int t, int i) __device__ __attribute__((always_inline)) {
-    const int te = min(t, ntiles - 1);
-    const T* src = gsrc + (int64_t)te * BN * kv_row;
-    const int rmax = min(BN - 1, Skv - 1 - te * BN);
-    const uint32_t lds = lds_addr(gdst + (uint32_t)(t % NSLOT) * TILE) + (uint32_t)gw * 1024;
-    lds_dma16(src, (uint32_t)min(i * WROWS + rl, rmax) * row_bytes + cbyte, lds + i * 4096);
+  auto loader = [&](auto is_v) __device__ __attribute__((always_inline)) {
+    constexpr bool IS_V = decltype(is_v)::value;
+    constexpr int DL = IS_V ? DV : D, CPR = DL / 8, WROWS = 256 / CPR;
+    constexpr int TL = BN * DL;
+    const int rl = gw * (64 / CPR) + lane / CPR;
+    auto key = [](int r) { return IS_V ? Swz<DL>::v_key(r) : Swz<DL>::k_key(r); };
+    const uint32_t cbyte = (uint32_t)((((lane % CPR) ^ key(rl)) << 3) * sizeof(T));
+    const T* gsrc = IS_V ? vbase : kbase;
+    T* gdst = IS_V ? v_lds : k_lds;
+    return [=](int t, int i) __device__ __attribute__((always_inline)) {
+      const int te = min(t, ntiles - 1);
+      const T* src = gsrc + (int64_t)te * BN * kv_row;
+      const int rmax = min(BN - 1, Skv - 1 - te * BN);
+      const uint32_t lds = lds_addr(gdst + (uint32_t)(t % NSLOT) * TL) + (uint32_t)gw * 1024;
+      const int r = i * WROWS + rl;
+      const uint32_t cb =
+          WROWS % 16 == 0 ? cbyte : (uint32_t)((((lane % CPR) ^ key(r)) << 3) * sizeof(T));
+      lds_dma16(src, (uint32_t)min(r, rmax) * row_bytes + cb, lds + i * 4096);
+    };
   };
+  const auto load_window_v = loader(std::integral_constant<bool, true>());
+  const auto load_window_k = loader(std::integral_constant<bool, false>());
   auto load_tile = [&](int t) __device__ __attribute__((always_inline)) {
+    if (grp_a) {
 #pragma unroll
-    for (int i = 0; i < NW; ++i) load_window(t, i);
+      for (int i = 0; i < NW_V; ++i) load_window_v(t, i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NW_K; ++i) load_window_k(t, i);
+    }
   };
-  // End of an MFMA phase: every tile this wavefront loaded earlier has
-  // landed; the WPW windows issued in this phase may stay in flight.
-  auto wait_loads = [&]() __device__ __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(0x0F70 | WPW);  // vmcnt(WPW)
+  // End of an MFMA phase with NWL windows issued in it: every tile this
+  // wavefront loaded earlier has landed; those NWL may stay in flight.
+  auto wait_loads = [&](auto nwl) __device__ __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0F70 | decltype(nwl)::value);  // vmcnt(NWL)
   };
 
   f32x16 acc_o[DBLK];
@@ -290,7 +313,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int db = 0; db < DBLK; ++db) {
     const int dim = db * 32 + 16 * (grp16 & 1) + 4 * (j16 & 3);
-    voff[db] = vrow * D + ((((dim >> 3) ^ Swz<D>::v_key(vrow)) << 3) | (dim & 7));
+    voff[db] = vrow * DV + ((((dim >> 3) ^ Swz<DV>::v_key(vrow)) << 3) | (dim & 7));
   }
 
   // Operand reads: `vb0` / `kb0` are the LDS byte addresses of this lane's
@@ -313,8 +336,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // A operand of the O^T update: 8 keys (16 ks + 8 rr + ..) of dim block db,
   // two 64-bit transpose reads assembled by whole-register moves
   auto read_vt = [&](uint32_t vb, int ks) __device__ __attribute__((always_inline)) -> V8 {
-    const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks) * D * 2));
-    const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks + 8) * D * 2));
+    const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks) * DV * 2));
+    const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks + 8) * DV * 2));
     const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
     const u32x4 w = {y0.x, y0.y, y1.x, y1.y};
     return __builtin_bit_cast(V8, w);
@@ -335,13 +358,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto mfma_phase = [&](auto do_o, auto do_s, auto ld, auto vslot, auto kslot, int lt)
       __device__ __attribute__((always_inline)) {
     constexpr bool DO_O = decltype(do_o)::value, DO_S = decltype(do_s)::value;
-    constexpr bool LD = decltype(ld)::value;
+    constexpr int LD = decltype(ld)::value;  // 0: no loads, 1: V windows, 2: K windows
+    constexpr int NWL = LD == 1 ? NW_V : LD == 2 ? NW_K : 1;
     constexpr int J = BN / 16;                             // 16-key steps per tile
     constexpr int KS4 = KSTEPS / J;                        // head-dim steps per 16-key step
     constexpr int WO = DO_O ? DBLK : 0, WS = DO_S ? KS4 * NKB : 0;
     constexpr int W = WO + WS;                             // MFMAs per 16-key step
     constexpr int N = J * W;
-    constexpr int LDSTEP = N / NW, LDPOS = LDSTEP > 5 ? 5 : LDSTEP - 1;
+    constexpr int LDSTEP = N / NWL, LDPOS = LDSTEP > 5 ? 5 : LDSTEP - 1;
     static_assert(KSTEPS % J == 0, "head-dim steps per 16-key step");
     if (DO_S) {
 #pragma unroll
@@ -350,8 +374,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // slot offsets: immediate DS offsets when the slot is a compile-time
     // constant (the unrolled loop), one add per address otherwise
     uint32_t vb[DBLK], kb[KSTEPS];
-    const uint32_t vso = (uint32_t)(int)vslot * TILE * (uint32_t)sizeof(T);
-    const uint32_t kso = (uint32_t)(int)kslot * TILE * (uint32_t)sizeof(T);
+    const uint32_t vso = (uint32_t)(int)vslot * TILE_V * (uint32_t)sizeof(T);
+    const uint32_t kso = (uint32_t)(int)kslot * TILE_K * (uint32_t)sizeof(T);
 #pragma unroll
     for (int db = 0; db < DBLK; ++db) vb[db] = vb0[db] + vso;
 #pragma unroll
@@ -385,11 +409,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // this MFMA
       if (n + PF < N) group_reads(n + PF);
-      if (LD && n % LDSTEP == LDPOS) load_window(lt, n / LDSTEP);
+      if (LD == 1 && n % LDSTEP == LDPOS) load_window_v(lt, n / LDSTEP);
+      if (LD == 2 && n % LDSTEP == LDPOS) load_window_k(lt, n / LDSTEP);
     }
   };
   typedef std::integral_constant<bool, true> yes;
   typedef std::integral_constant<bool, false> no;
+  typedef std::integral_constant<int, 0> ld_none;
+  typedef std::integral_constant<int, 1> ld_v;
+  typedef std::integral_constant<int, 2> ld_k;
+  typedef std::integral_constant<int, NW_V> nw_v;
+  typedef std::integral_constant<int, NW_K> nw_k;
 
   // P = exp2(scale_log2 * s + neg_mc) of the tile in acc_s into pb (the
   // MFMA operand, rounded to the storage type); returns this lane's partial
@@ -489,36 +519,37 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   typedef std::integral_constant<int, 2> s2;
   if constexpr (NSLOT == 3) {
   // one loop step: softmax phase, then MFMA phase (slots as constants)
-  auto step = [&](auto vslot, auto kslot, int t_soft, int t_load) __device__ __attribute__((always_inline)) {
+  auto step = [&](auto ld, auto nwl, auto vslot, auto kslot, int t_soft, int t_load)
+      __device__ __attribute__((always_inline)) {
     softmax(t_soft);
     lds_barrier();
-    mfma_phase(yes(), yes(), yes(), vslot, kslot, t_load);
-    wait_loads();
+    mfma_phase(yes(), yes(), ld, vslot, kslot, t_load);
+    wait_loads(nwl);
     lds_barrier();
   };
   if (grp_a) {
     if (ntiles > 0) {
-      mfma_phase(no(), yes(), yes(), s0(), s0(), 1);
-      wait_loads();
+      mfma_phase(no(), yes(), ld_v(), s0(), s0(), 1);
+      wait_loads(nw_v());
     }
     lds_barrier();
     // step tau: softmax(tau) | O(tau) (V slot tau % 3), S(tau + 1) (K slot (tau + 1) % 3)
     int tau = 0;
     for (; tau + 3 < ntiles; tau += 3) {
-      step(s0(), s1(), tau, tau + 2);
-      step(s1(), s2(), tau + 1, tau + 3);
-      step(s2(), s0(), tau + 2, tau + 4);
+      step(ld_v(), nw_v(), s0(), s1(), tau, tau + 2);
+      step(ld_v(), nw_v(), s1(), s2(), tau + 1, tau + 3);
+      step(ld_v(), nw_v(), s2(), s0(), tau + 2, tau + 4);
     }
     if (tau + 1 < ntiles) {
-      step(s0(), s1(), tau, tau + 2);
+      step(ld_v(), nw_v(), s0(), s1(), tau, tau + 2);
       ++tau;
-      if (tau + 1 < ntiles) step(s1(), s2(), tau, tau + 2);
+      if (tau + 1 < ntiles) step(ld_v(), nw_v(), s1(), s2(), tau, tau + 2);
     }
     if (ntiles > 0) {
       const int t = ntiles - 1;
       softmax(t);
       lds_barrier();
-      mfma_phase(yes(), no(), no(), t % 3, 0, -1);
+      mfma_phase(yes(), no(), ld_none(), t % 3, 0, -1);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
     }
@@ -526,27 +557,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   } else {
     lds_barrier();  // phase 0: group A computes S(0)
     if (ntiles > 0) {
-      mfma_phase(no(), yes(), yes(), s0(), s0(), 2);
-      wait_loads();
+      mfma_phase(no(), yes(), ld_k(), s0(), s0(), 2);
+      wait_loads(nw_k());
     }
     lds_barrier();
     // step tau: softmax(tau - 1) | O(tau - 1) (V slot (tau - 1) % 3), S(tau) (K slot tau % 3)
     int tau = 1;
     for (; tau + 2 < ntiles; tau += 3) {
-      step(s0(), s1(), tau - 1, tau + 2);
-      step(s1(), s2(), tau, tau + 3);
-      step(s2(), s0(), tau + 1, tau + 4);
+      step(ld_k(), nw_k(), s0(), s1(), tau - 1, tau + 2);
+      step(ld_k(), nw_k(), s1(), s2(), tau, tau + 3);
+      step(ld_k(), nw_k(), s2(), s0(), tau + 1, tau + 4);
     }
     if (tau < ntiles) {
-      step(s0(), s1(), tau - 1, tau + 2);
+      step(ld_k(), nw_k(), s0(), s1(), tau - 1, tau + 2);
       ++tau;
-      if (tau < ntiles) step(s1(), s2(), tau - 1, tau + 2);
+      if (tau < ntiles) step(ld_k(), nw_k(), s1(), s2(), tau - 1, tau + 2);
     }
     if (ntiles > 0) {
       const int t = ntiles;
       softmax(t - 1);
       lds_barrier();
-      mfma_phase(yes(), no(), no(), (t - 1) % 3, 0, -1);
+      mfma_phase(yes(), no(), ld_none(), (t - 1) % 3, 0, -1);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
     }
@@ -559,14 +590,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // at the end of phase 2t + 1.  Either way the slot's previous tile (t - 2)
   // was last read in the phase before the issue.
   if (grp_a) {
-    if (ntiles > 0) mfma_phase(no(), yes(), no(), s0(), s0(), -1);  // phase 0: S(0)
+    if (ntiles > 0) mfma_phase(no(), yes(), ld_none(), s0(), s0(), -1);  // phase 0: S(0)
     lds_barrier();
     // step tau: softmax(tau) | O(tau) (V slot tau % 2), S(tau + 1), V(tau + 1)
     auto step_a = [&](auto vslot, auto kslot, int tau) __device__ __attribute__((always_inline)) {
       softmax(tau);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): V(tau) has landed
       lds_barrier();
-      mfma_phase(yes(), yes(), yes(), vslot, kslot, tau + 1);
+      mfma_phase(yes(), yes(), ld_v(), vslot, kslot, tau + 1);
       lds_barrier();
     };
     int tau = 0;
@@ -583,20 +614,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       softmax(t);
       __builtin_amdgcn_s_waitcnt(0x0F70);
       lds_barrier();
-      mfma_phase(yes(), no(), no(), t % 2, 0, -1);
+      mfma_phase(yes(), no(), ld_none(), t % 2, 0, -1);
       lds_barrier();
     }
     lds_barrier();  // softmax phase of step ntiles (nothing left to do)
   } else {
     lds_barrier();  // phase 0: group A computes S(0)
-    if (ntiles > 0) mfma_phase(no(), yes(), no(), s0(), s0(), -1);  // phase 1: S(0)
+    if (ntiles > 0) mfma_phase(no(), yes(), ld_none(), s0(), s0(), -1);  // phase 1: S(0)
     lds_barrier();
     // step tau: softmax(tau - 1), K(tau + 1) | O(tau - 1) (V slot (tau - 1) % 2), S(tau)
     auto step_b = [&](auto vslot, auto kslot, int tau) __device__ __attribute__((always_inline)) {
       load_tile(tau + 1);
       softmax(tau - 1);
       lds_barrier();
-      mfma_phase(yes(), yes(), no(), vslot, kslot, -1);
+      mfma_phase(yes(), yes(), ld_none(), vslot, kslot, -1);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K(tau + 1) has landed
       lds_barrier();
     };
@@ -613,7 +644,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int t = ntiles;
       softmax(t - 1);
       lds_barrier();
-      mfma_phase(yes(), no(), no(), (t - 1) % 2, 0, -1);
+      mfma_phase(yes(), no(), ld_none(), (t - 1) % 2, 0, -1);
       lds_barrier();
     }
   }
@@ -624,7 +655,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const float l_tot = pair_sum(l_run);
   const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (qi < Sq) {
-    T* orow = o + ((int64_t)bb * Sq + qi) * q_row + (int64_t)hq * D;
+    T* orow = o + ((int64_t)bb * Sq + qi) * q_row + (int64_t)hq * D + dv0;
 #pragma unroll
     for (int db = 0; db < DBLK; ++db) {
 #pragma unroll
@@ -636,26 +667,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         *reinterpret_cast<uint2*>(orow + d) = *reinterpret_cast<uint2*>(vals);
       }
     }
-    if (half == 0)
+    if (half == 0 && dv0 == 0)
       lse[((int64_t)bb * H + hq) * Sq + qi] =
           l_tot > 0.0f ? m_run * scale_log2 + __builtin_amdgcn_logf(l_tot) : -INFINITY;
   }
 }
 
-template <typename T, int D, int BN, bool SOFTCAP>
+template <typename T, int D, int DV, int BN, bool SOFTCAP>
 static void launch_k(const void* q, const void* k, const void* v, void* o, float* lse, int B,
                      int Sq, int Skv, int H, int Hkv, bool causal, float sl2, float cap_scale,
                      float cap_log2, hipStream_t s) {
   constexpr int BM = 256;
   const int nqb = (Sq + BM - 1) / BM;
-  const int64_t total = (int64_t)nqb * H * B;
+  const int64_t total = (int64_t)nqb * H * B * (D / DV);
   dim3 grid((unsigned)total), block(512);
   if (causal)
-    mha_fwd_kernel<T, D, true, BN, SOFTCAP><<<grid, block, 0, s>>>(
+    mha_fwd_kernel<T, D, DV, true, BN, SOFTCAP><<<grid, block, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
         static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, sl2, nqb, cap_scale, cap_log2);
   else
-    mha_fwd_kernel<T, D, false, BN, SOFTCAP><<<grid, block, 0, s>>>(
+    mha_fwd_kernel<T, D, DV, false, BN, SOFTCAP><<<grid, block, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
         static_cast<T*>(o), lse, B, Sq, Skv, H, Hkv, sl2, nqb, cap_scale, cap_log2);
 }
@@ -665,12 +696,16 @@ static int launch_w(const void* q, const void* k, const void* v, void* o, float*
                     int Sq, int Skv, int H, int Hkv, bool causal, float scale, float softcap,
                     hipStream_t s) {
   constexpr float kLog2e = 1.4426950408889634f;
+  // D = 128: 128-key tiles, two slots; D = 64: 64-key tiles, three slots;
+  // D = 256: two workgroups per query block, 128 value columns each
+  constexpr int DV = D == 256 ? 128 : D;
+  constexpr int BN = D == 128 ? 128 : 64;
   if (softcap > 0.0f)
-    launch_k<T, D, (D == 128 ? 128 : 64), true>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, 1.0f, scale / softcap,
-                             softcap * kLog2e, s);
+    launch_k<T, D, DV, BN, true>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, 1.0f,
+                                 scale / softcap, softcap * kLog2e, s);
   else
-    launch_k<T, D, (D == 128 ? 128 : 64), false>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale * kLog2e, 0.0f,
-                              0.0f, s);
+    launch_k<T, D, DV, BN, false>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal,
+                                  scale * kLog2e, 0.0f, 0.0f, s);
   return launch_status();
 }
 
@@ -682,6 +717,8 @@ static int dispatch_d(int D, const void* q, const void* k, const void* v, void* 
     return launch_w<T, 128>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
   if (D == 64)
     return launch_w<T, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
+  if (D == 256)
+    return launch_w<T, 256>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
   return TILEOPS_ESHAPE;
 }
 
@@ -695,7 +732,7 @@ extern "C" int tileops_mha_fwd(const void* q, const void* k, const void* v, void
                                int64_t D, int causal, float scale, float softcap, int dtype,
                                void* stream) {
   if (B < 0 || Sq < 0 || Skv < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0) return TILEOPS_ESHAPE;
-  if (D != 64 && D != 128) return TILEOPS_ESHAPE;
+  if (D != 64 && D != 128 && D != 256) return TILEOPS_ESHAPE;
   if (B > INT32_MAX || Sq > INT32_MAX || Skv > INT32_MAX || H > 65535) return TILEOPS_ESHAPE;
   if (causal && Sq > Skv) return TILEOPS_ESHAPE;
   if (dtype != TILEOPS_F16 && dtype != TILEOPS_BF16) return TILEOPS_EINVAL;
@@ -705,7 +742,8 @@ extern "C" int tileops_mha_fwd(const void* q, const void* k, const void* v, void
   if (!q || !k || !v || !o || !lse) return TILEOPS_ENULL;
   if (!host_aligned16(q) || !host_aligned16(k) || !host_aligned16(v) || !host_aligned16(o))
     return TILEOPS_EINVAL;
-  if (((Sq + 127) / 128) * H * B > (int64_t)UINT32_MAX) return TILEOPS_ESHAPE;
+  // grid: (Sq / 256) query blocks x H x B (x 2 for D = 256), indexed in int
+  if (((Sq + 255) / 256) * H * B * (D == 256 ? 2 : 1) > (int64_t)INT32_MAX) return TILEOPS_ESHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TILEOPS_BF16)
     return mha::dispatch_d<bf16>((int)D, q, k, v, o, lse, (int)B, (int)Sq, (int)Skv, (int)H,

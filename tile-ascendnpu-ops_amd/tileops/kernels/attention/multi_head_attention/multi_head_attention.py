@@ -94,8 +94,8 @@ class GQAPrefillFwdKernel(Kernel):
             raise ValueError(
                 f"{self.__class__.__name__} only supports dtypes [{supported}], got {dtype}"
             )
-        if dim not in (64, 128):
-            raise ValueError(f"{self.__class__.__name__} supports dim 64 or 128, got {dim}")
+        if dim not in (64, 128, 256):
+            raise ValueError(f"{self.__class__.__name__} supports dim 64, 128 or 256, got {dim}")
         if not (0.0 <= softcap < float("inf")):
             raise ValueError(f"{self.__class__.__name__}: softcap must be finite and >= 0 (got {softcap})")
         self.batch = batch
