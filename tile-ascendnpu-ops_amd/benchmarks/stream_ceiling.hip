@@ -4,7 +4,11 @@
 // add/lerp bcast_vec_kernel, isfp_vec_kernel), non-temporal loads and stores,
 // 1 GiB per stream so that the 256 MB Infinity Cache cannot serve it.
 //
-//   stream_ceiling [--iters N]
+//   stream_ceiling [--iters N] [--mib M]
+//
+// M (default 1024) is the size of each stream in MiB; below 1 GiB the
+// launches cycle through enough copies of the buffers that the working set
+// stays at 4 GiB or more, so that the Infinity Cache cannot serve a repeat.
 //
 // prints one line per mix: bytes moved per launch, mean kernel time over N
 // launches (HIP events), GB/s and the fraction of the 8 TB/s peak.  Two
@@ -52,21 +56,34 @@ __global__ __launch_bounds__(256) void stream_kernel(const u32x4* __restrict__ s
 
 int main(int argc, char** argv) {
   int iters = 20;
-  for (int a = 1; a + 1 < argc; ++a)
+  long long mib = 1024;
+  for (int a = 1; a + 1 < argc; ++a) {
     if (!strcmp(argv[a], "--iters")) iters = atoi(argv[a + 1]);
-  const long long bytes = 1ll << 30, npack = bytes / 16;
+    if (!strcmp(argv[a], "--mib")) mib = atoll(argv[a + 1]);
+  }
+  if (iters < 1 || mib < 8 || mib > 8192 || (mib & 7)) {
+    fprintf(stderr, "--iters >= 1, --mib a multiple of 8 in [8, 8192]\n");
+    return 1;
+  }
+  const long long bytes = mib << 20, npack = bytes / 16;
   const unsigned grid = (unsigned)(npack / 256);  // a multiple of 8
-  u32x4 *s0, *s1, *d0, *d1;
-  CHECK(hipMalloc(&s0, bytes));
-  CHECK(hipMalloc(&s1, bytes));
-  CHECK(hipMalloc(&d0, bytes));
-  CHECK(hipMalloc(&d1, bytes));
-  CHECK(hipMemset(s0, 1, bytes));
-  CHECK(hipMemset(s1, 2, bytes));
+  const int nsets = mib >= 1024 ? 1 : (int)((1024 + mib - 1) / mib);
+  constexpr int kMaxSets = 128;
+  u32x4 *s0[kMaxSets], *s1[kMaxSets], *d0[kMaxSets], *d1[kMaxSets];
+  for (int k = 0; k < nsets; ++k) {
+    CHECK(hipMalloc(&s0[k], bytes));
+    CHECK(hipMalloc(&s1[k], bytes));
+    CHECK(hipMalloc(&d0[k], bytes));
+    CHECK(hipMalloc(&d1[k], bytes));
+    CHECK(hipMemset(s0[k], 1, bytes));
+    CHECK(hipMemset(s1[k], 2, bytes));
+  }
+  int cur = 0;  // buffer set of the next launch
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
-  printf("# 1 GiB per stream, %d timed launches after 3 warm-up; peak 8000 GB/s\n", iters);
+  printf("# %lld MiB per stream (%d buffer sets cycled), %d timed launches after 3 warm-up; "
+         "peak 8000 GB/s\n", mib, nsets, iters);
   printf("%-28s %12s %10s %10s %7s\n", "mix", "bytes", "us", "GB/s", "peak");
   auto run = [&](const char* name, double moved, auto launch) -> int {
     for (int i = 0; i < 3; ++i) launch();
@@ -81,11 +98,17 @@ int main(int argc, char** argv) {
     printf("%-28s %12.0f %10.2f %10.1f %6.1f%%\n", name, moved, us, gbs, gbs / 80.0);
     return 0;
   };
-#define MIX(R, W)                                                                             \
-  if (run(#R "R/" #W "W", (double)(R + W) * bytes,                                           \
-          [&] { stream_kernel<R, W, false><<<grid, 256>>>(s0, s1, d0, d1, npack); }) ||       \
-      run(#R "R/" #W "W xcd-contiguous", (double)(R + W) * bytes,                            \
-          [&] { stream_kernel<R, W, true><<<grid, 256>>>(s0, s1, d0, d1, npack); }))          \
+#define MIX(R, W)                                                                              \
+  if (run(#R "R/" #W "W", (double)(R + W) * bytes,                                            \
+          [&] {                                                                               \
+            stream_kernel<R, W, false><<<grid, 256>>>(s0[cur], s1[cur], d0[cur], d1[cur], npack); \
+            cur = (cur + 1) % nsets;                                                          \
+          }) ||                                                                               \
+      run(#R "R/" #W "W xcd-contiguous", (double)(R + W) * bytes,                             \
+          [&] {                                                                               \
+            stream_kernel<R, W, true><<<grid, 256>>>(s0[cur], s1[cur], d0[cur], d1[cur], npack); \
+            cur = (cur + 1) % nsets;                                                          \
+          }))                                                                                 \
     return 1;
   MIX(1, 0)
   MIX(0, 1)
@@ -94,12 +117,16 @@ int main(int argc, char** argv) {
   MIX(1, 2)
   MIX(2, 2)
 #undef MIX
-  if (run("hipMemcpy device to device", 2.0 * bytes,
-          [&] { (void)hipMemcpyAsync(d0, s0, bytes, hipMemcpyDeviceToDevice, 0); }))
+  if (run("hipMemcpy device to device", 2.0 * bytes, [&] {
+        (void)hipMemcpyAsync(d0[cur], s0[cur], bytes, hipMemcpyDeviceToDevice, 0);
+        cur = (cur + 1) % nsets;
+      }))
     return 1;
-  CHECK(hipFree(s0));
-  CHECK(hipFree(s1));
-  CHECK(hipFree(d0));
-  CHECK(hipFree(d1));
+  for (int k = 0; k < nsets; ++k) {
+    CHECK(hipFree(s0[k]));
+    CHECK(hipFree(s1[k]));
+    CHECK(hipFree(d0[k]));
+    CHECK(hipFree(d1[k]));
+  }
   return 0;
 }
