@@ -335,3 +335,137 @@ def test_setup_gpu_label_from_gpu_agents(monkeypatch):
 
     monkeypatch.setattr(setup_info.subprocess, "run", lambda *a, **k: _Res())
     assert setup_info._gpu_info() == "AMD Instinct MI355X (gfx950) x 1"
+
+
+def test_runner_with_counters_sets_the_benchmark_env(tmp_path, monkeypatch):
+    calls = []
+    rec = _record("HardswishFwdOp", "a", "fc-wide", 80.0)
+    rec["result"].update({"HBM bytes (counters)": 60_000_000, "HBM(TB/s, counters)": 6.0,
+                          "MFMA busy(%)": 0.0})
+    _fake_stages(monkeypatch, JUNIT_OK, [rec], calls)
+    run, run_dir, code = runner.run_operator("HardswishFwdOp", reports_dir=tmp_path / "r",
+                                             with_counters=True)
+    assert code == 0
+    assert calls[1]["env"]["TILEOPS_ROCPROF_COUNTERS"] == "1"
+    case = run["performance"]["cases"][0]
+    assert case["hbm_bytes_measured"] == 60_000_000 and case["mfma_busy_percent"] == 0.0
+    md = (run_dir / "report.md").read_text()
+    assert "HBM (TB/s, counters)" in md and "MFMA busy (%)" in md
+    # bandwidth 6 TB/s x 10 us = 60,000,000 roofline bytes: ratio 1.000
+    assert "1.000" in md
+    calls.clear()
+    runner.run_operator("HardswishFwdOp", reports_dir=tmp_path / "r2")
+    assert "TILEOPS_ROCPROF_COUNTERS" not in calls[1]["env"]
+
+
+def test_counter_totals_from_a_pmc_database(tmp_path):
+    import sqlite3
+
+    db = tmp_path / "pmc_results.db"
+    con = sqlite3.connect(db)
+    con.execute("create table counters_collection (kernel_name text, counter_name text, value real)")
+    con.executemany("insert into counters_collection values (?, ?, ?)", [
+        ("tileops::gdn::gdn_prep_kernel(...)", "FETCH_SIZE", 100.0),
+        ("tileops::gdn::gdn_recur_kernel(...)", "FETCH_SIZE", 50.0),
+        ("tileops::gdn::gdn_prep_kernel(...)", "FETCH_SIZE", 100.0),
+        ("void at::native::copy_kernel", "FETCH_SIZE", 999.0),
+        ("tileops::gdn::gdn_recur_kernel(...)", "GRBM_GUI_ACTIVE", 8000.0),
+    ])
+    con.commit()
+    con.close()
+    tot = rp.read_counter_totals(str(db), "tileops")
+    assert tot == {"FETCH_SIZE": 250.0, "GRBM_GUI_ACTIVE": 8000.0}
+    assert rp.read_counter_totals(str(db), "gdn_recur") == {"FETCH_SIZE": 50.0,
+                                                           "GRBM_GUI_ACTIVE": 8000.0}
+
+
+def test_profile_attaches_counters_when_asked(monkeypatch):
+    """rocprof mode with TILEOPS_ROCPROF_COUNTERS=1: the counter summary lands in
+    the result next to the latency (measured bytes over the latency)."""
+    meta = {"kernel_name_resolved": "tileops", "kernels": []}
+    monkeypatch.setattr(rp, "bench_kernel_rocprof", lambda f, args=(): (0.01, "/tmp", dict(meta)))
+    monkeypatch.setattr(rp, "bench_kernel_counters",
+                        lambda f, args=(), kernel_name=None: {"hbm_bytes": 80_000_000,
+                                                              "mfma_busy_percent": 12.5})
+    monkeypatch.setattr(bb, "get_device_backend", lambda: type("B", (), {"synchronize": lambda s: None})())
+    monkeypatch.setenv("TILEOPS_ROCPROF_COUNTERS", "1")
+
+    class _Bench(bb.BenchmarkBase):
+        def calculate_flops(self):
+            return None
+
+        def calculate_memory(self):
+            return 80_000_000
+
+    res = _Bench(type("W", (), {"dtype": torch.float16})()).profile(lambda: None, mode="rocprof")
+    assert res["prof_mode"] == "rocprof"
+    assert res["HBM bytes (counters)"] == 80_000_000
+    assert res["HBM(TB/s, counters)"] == pytest.approx(8.0)  # 80 MB in 10 us
+    assert res["MFMA busy(%)"] == 12.5
+
+
+def test_profile_records_why_rocprof_or_counters_failed(monkeypatch):
+    """A rocprof failure falls back to events timing with its reason in the
+    result; a counter failure keeps the rocprof timing and records the error;
+    the analyzer turns both into warnings."""
+    monkeypatch.setattr(bb, "get_device_backend", lambda: type("B", (), {"synchronize": lambda s: None})())
+    monkeypatch.setattr(bb, "bench_kernel", lambda f, args=(): 0.02)
+
+    class _Bench(bb.BenchmarkBase):
+        def calculate_flops(self):
+            return None
+
+        def calculate_memory(self):
+            return 1_000_000
+
+    bench = _Bench(type("W", (), {"dtype": torch.float16})())
+
+    def _fail(f, args=()):
+        raise ValueError("0 matching dispatches do not split into 15 calls")
+
+    monkeypatch.setattr(rp, "bench_kernel_rocprof", _fail)
+    res = bench.profile(lambda: None, mode="rocprof")
+    assert res["prof_mode"] == "events" and "rocprof" not in res
+    assert "0 matching dispatches" in res["rocprof_fallback"]
+
+    meta = {"kernels": [{"name": "tileops::k", "avg_us": 10.0}]}
+    monkeypatch.setattr(rp, "bench_kernel_rocprof", lambda f, args=(): (0.01, "/tmp", dict(meta)))
+
+    def _ctr_fail(f, args=(), kernel_name=None):
+        raise RuntimeError("rocprofv3 --pmc failed (exit 1)")
+
+    monkeypatch.setattr(rp, "bench_kernel_counters", _ctr_fail)
+    monkeypatch.setenv("TILEOPS_ROCPROF_COUNTERS", "1")
+    res2 = bench.profile(lambda: None, mode="rocprof")
+    assert res2["prof_mode"] == "rocprof" and res2["latency_us"] == pytest.approx(10.0)
+    assert "--pmc failed" in res2["rocprof"]["counters_error"]
+    assert "HBM bytes (counters)" not in res2
+
+    bench = {"status": "present", "profiling_mode_requested": "rocprof", "records": [
+        {"operator": "Op", "case_id": "a", "label": "big", "result": res, "tag": "tileops"},
+        {"operator": "Op", "case_id": "b", "label": "big", "result": res2, "tag": "tileops"}]}
+    corr = {"status": "passed", "tests": 1, "passed": 1, "failed": 0, "errors": 0, "cases": []}
+    run = analyzer.analyze_run(operator="Op", correctness=corr, correctness_exit_code=0,
+                               benchmark=bench, benchmark_exit_code=0)
+    text = " ".join(run["warnings"])
+    assert "requested rocprof but recorded events (ValueError: 0 matching" in text
+    assert "counter collection failed (RuntimeError: rocprofv3 --pmc failed" in text
+
+
+def test_declared_kernel_regexes_match_mangled_and_demangled_names():
+    """rocprofv3 stores the demangled name where its demangler succeeds and the
+    mangled one where it does not; every declared regex matches both."""
+    import re
+
+    from tileops.kernels.attention.multi_head_attention.multi_head_attention import (
+        GQAPrefillFwdKernel,
+    )
+    from tileops.kernels.linear_attention.gdn_prefill.gdn_prefill import GDNPrefillFwdKernel
+
+    gdn = re.compile(GDNPrefillFwdKernel.profile_kernel_name)
+    assert gdn.search("tileops::gdn::gdn_recur_kernel(bool _Accum const*, _S, _P)")
+    assert gdn.search("_ZN7tileops3gdn15gdn_prep_kernelEPKDF16bS3_")
+    mha = re.compile(GQAPrefillFwdKernel.profile_kernel_name)
+    assert mha.search("_ZN7tileops3mha14mha_fwd_kernelIDF16_Li64ELi64ELb1ELi64ELb0EEEvPKT_")
+    assert mha.search("void tileops::mha::mha_fwd_kernel<float, 64>(float const*)")
+    assert not mha.search("void at::native::elementwise_kernel<128, 4>()")

@@ -92,24 +92,32 @@ def test_reference_test_imports_resolve(module, name):
 
 # Representative mangled names of the device kernels in libtileops_hip.so, by the
 # Kernel classes that launch them.
+# rocprofv3 records the demangled name where its demangler succeeds and the
+# mangled one where it fails (_Float16 / __bf16 template arguments): both forms
 _MANGLED = {
     "unary": ["_ZN7tileops16unary_vec_kernelIDF16_Li0EEEvPKT_PS1_lffi",
-              "_ZN7tileops19unary_scalar_kernelIfLi2EEEvPKT_PS1_llffi"],
+              "_ZN7tileops19unary_scalar_kernelIfLi2EEEvPKT_PS1_llffi",
+              "void tileops::unary_scalar_kernel<float, 2>(float const*, float*, long, long)"],
     "isfp": ["_ZN7tileops15isfp_vec_kernelIfLi0EEEvPKT_Phl",
              "_ZN7tileops18isfp_scalar_kernelIfLi1EEEvPKT_Phll"],
     "gated": ["_ZN7tileops21gated_gelu_vec_kernelIDF16b_Li0ELi2EEEvPKT_PS1_ll",
-              "_ZN7tileops24gated_gelu_scalar_kernelIfLi1EEEvPKT_PS1_ll"],
+              "_ZN7tileops24gated_gelu_scalar_kernelIfLi1EEEvPKT_PS1_ll",
+              "void tileops::gated_gelu_vec_kernel<float, 0, 2>(float const*, float*, long, long)"],
     "bcast": ["_ZN7tileops16bcast_vec_kernelIfLi0EEEvPKT_S3_S3_PS1_lf",
               "_ZN7tileops18bcast_inner_kernelIDF16_Li1EjEEvPKT_S3_S3_PS1_T1_S5_f",
               "_ZN7tileops16bcast_any_kernelIfLi2EEEvPKT_S3_S3_PS1_llfNS_9BcastDescE"],
     "bitnot": ["_ZN7tileops17bitnot_vec_kernelEPKDv4_jPS0_lj",
                "_ZN7tileops18bitnot_byte_kernelEPKhPhllj"],
     "ln": ["_ZN7tileops24fused_add_ln_wave_kernelIDF16b_Li2ELi16ELi4EEEvPKT_S3_PKvS5_PS1_S6_lf",
+           "_ZN7tileops25fused_add_ln_block_kernelIffLi5EEEvPKT_S3_PKT0_S6_PS1_S7_ifb",
+           "tileops::fused_add_ln_block_kernel<float, float, 5>(float const*)",
            "_ZN7tileops27fused_add_ln_generic_kernelIfLi0EEEvPKT_S3_PKvS5_PS1_S6_llf"],
-    "row": ["_ZN7tileops17row_reduce_kernelIfLi0ELi1ELi4ELb1EEEvPKT_Pvll"],
+    "row": ["_ZN7tileops17row_reduce_kernelIfLi0ELi1ELi4ELb1EEEvPKT_Pvll",
+            "void tileops::row_reduce_kernel<float, 0, 1, 4, true>(float const*, void*, long, long)"],
     "mha": ["_ZN7tileops3mha14mha_fwd_kernelIDF16b_Li128ELb1ELi64ELb0EEEvPKT_S4_S4_PS2_Pfiiiiififf"],
     "gdn": ["_ZN7tileops3gdn15gdn_prep_kernelEPKDF16bS2_PKfS4_Phiiiif",
-            "_ZN7tileops3gdn16gdn_recur_kernelEPKDF16bPKhS2_PS0_PfS7_iiii"],
+            "_ZN7tileops3gdn16gdn_recur_kernelEPKDF16bPKhS2_PS0_PfS7_iiii",
+            "tileops::gdn::gdn_recur_kernel(bool _Accum const*, _S, _P, float const)"],
     "gla": ["_ZN7tileops3gla17gla_decode_kernelIDF16bLb1EEEvPKT_S4_S4_S4_PKfPS2_Pfiiif"],
 }
 

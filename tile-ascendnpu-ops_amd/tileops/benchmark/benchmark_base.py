@@ -187,9 +187,11 @@ def bench_kernel(
 def _bench_with_mode(
     functor: Callable, args: tuple = (), mode: Optional[str] = None
 ) -> tuple[float, str, Optional[dict]]:
-    """``(latency_ms, prof_mode, rocprof_metadata)``.  ``rocprof`` falls back
-    to ``events`` (with a warning) when the functor cannot be rebuilt in a
-    child process or rocprofv3 is unavailable or fails."""
+    """``(latency_ms, prof_mode, metadata)``.  ``rocprof`` falls back to
+    ``events`` (with a warning) when the functor cannot be rebuilt in a child
+    process or rocprofv3 is unavailable or fails; the metadata is then
+    ``{"fallback_reason": ...}``.  A failed counter collection leaves the
+    rocprof timing and records ``counters_error`` in its metadata."""
     mode = _prof_mode(mode)
     if mode == "rocprof":
         from tileops.benchmark.rocprof import bench_kernel_rocprof
@@ -199,11 +201,21 @@ def _bench_with_mode(
             functor(*args)
             get_device_backend().synchronize()
             latency, _out, meta = bench_kernel_rocprof(functor, args=args)
-            return latency, "rocprof", meta
         except (TypeError, RuntimeError, ValueError, OSError) as e:
-            _logger.warning("rocprof profiling failed (%s: %s); falling back to events.",
-                            type(e).__name__, e)
-            return bench_kernel(functor, args=args), "events", None
+            reason = f"{type(e).__name__}: {e}"
+            _logger.warning("rocprof profiling failed (%s); falling back to events.", reason)
+            return bench_kernel(functor, args=args), "events", {"fallback_reason": reason[-1000:]}
+        if os.environ.get("TILEOPS_ROCPROF_COUNTERS") == "1":
+            from tileops.benchmark.rocprof import bench_kernel_counters
+
+            try:
+                meta["counters"] = bench_kernel_counters(
+                    functor, args=args, kernel_name=meta.get("kernel_name_resolved"))
+            except (TypeError, RuntimeError, ValueError, OSError) as e:
+                reason = f"{type(e).__name__}: {e}"
+                _logger.warning("counter collection failed (%s)", reason)
+                meta["counters_error"] = reason[-1000:]
+        return latency, "rocprof", meta
     return bench_kernel(functor, args=args), "events", None
 
 
@@ -228,8 +240,15 @@ class BenchmarkBase(Generic[W], ABC):
         with torch.no_grad():
             latency, prof_mode, meta = _bench_with_mode(functor, args=inputs, mode=mode)
         result = self._build_result(latency)
-        if meta is not None:
+        if meta is not None and prof_mode != "rocprof":
+            result["rocprof_fallback"] = meta.get("fallback_reason")
+        elif meta is not None:
             result["rocprof"] = meta
+            ctr = meta.get("counters")
+            if ctr:  # measured HBM traffic and MFMA busy (rocprofv3 counters)
+                result["HBM bytes (counters)"] = ctr["hbm_bytes"]
+                result["HBM(TB/s, counters)"] = ctr["hbm_bytes"] / (latency * 1e-3) * 1e-12
+                result["MFMA busy(%)"] = ctr["mfma_busy_percent"]
         result["prof_mode"] = prof_mode
         return result
 

@@ -68,7 +68,7 @@ class GQAPrefillFwdKernel(Kernel):
     """
 
     SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
-    profile_kernel_name = r"mha\d+mha_fwd_kernel"
+    profile_kernel_name = r"mha(?:::|\d+)mha_fwd_kernel"
 
     def __init__(
         self,

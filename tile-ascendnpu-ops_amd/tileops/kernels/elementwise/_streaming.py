@@ -36,7 +36,7 @@ class UnaryFwdKernel(Kernel):
 
     SUPPORTED_DTYPES = _FLOAT_DTYPES
     _unary_op: int = -1
-    profile_kernel_name = r"tileops\d+unary_(vec|scalar)_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)unary_(vec|scalar)_kernel"
 
     def __init__(self, N_total: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()
@@ -90,7 +90,7 @@ class PredicateFwdKernel(Kernel):
 
     SUPPORTED_DTYPES = _FLOAT_DTYPES
     _predicate: int = -1
-    profile_kernel_name = r"tileops\d+isfp_(vec|scalar)_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)isfp_(vec|scalar)_kernel"
 
     def __init__(self, N_total: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()
@@ -128,7 +128,7 @@ class GatedGeluFwdKernel(Kernel):
 
     SUPPORTED_DTYPES = _FLOAT_DTYPES
     _approx: int = 0
-    profile_kernel_name = r"tileops\d+gated_gelu_(vec|scalar)_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)gated_gelu_(vec|scalar)_kernel"
 
     def __init__(self, M: int, N: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()

@@ -39,7 +39,7 @@ class BroadcastFwdKernel(Kernel):
     and hand them to the C ABI as host arrays."""
 
     SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
-    profile_kernel_name = r"tileops\d+bcast_(vec|inner|any)_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)bcast_(vec|inner|any)_kernel"
 
     def _init_common(self, N_total: int, dtype: torch.dtype, config: Optional[dict]) -> None:
         if dtype not in self.SUPPORTED_DTYPES:

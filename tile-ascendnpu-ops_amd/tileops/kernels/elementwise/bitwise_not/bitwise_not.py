@@ -29,7 +29,7 @@ class BitwiseNotFwdKernel(Kernel):
     """
 
     SUPPORTED_DTYPES = BITWISE_DTYPES
-    profile_kernel_name = r"tileops\d+bitnot_(vec|byte)_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)bitnot_(vec|byte)_kernel"
 
     def __init__(self, N_total: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()

@@ -34,7 +34,7 @@ class GDNPrefillFwdKernel(Kernel):
     """
 
     SUPPORTED_DTYPES = (torch.bfloat16,)
-    profile_kernel_name = r"gdn\d+gdn_(prep|recur)_kernel"
+    profile_kernel_name = r"gdn(?:::|\d+)gdn_(prep|recur)_kernel"
 
     def __init__(
         self,

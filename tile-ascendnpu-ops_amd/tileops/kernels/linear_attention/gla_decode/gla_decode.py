@@ -54,7 +54,7 @@ class GLADecodeKernel(Kernel):
     """
 
     SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
-    profile_kernel_name = r"gla\d+gla_decode_kernel"
+    profile_kernel_name = r"gla(?:::|\d+)gla_decode_kernel"
 
     def __init__(
         self,

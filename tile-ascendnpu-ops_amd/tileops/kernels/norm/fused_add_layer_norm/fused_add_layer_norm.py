@@ -36,7 +36,7 @@ class FusedAddLayerNormKernel(Kernel):
     """
 
     SUPPORTED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
-    profile_kernel_name = r"tileops\d+fused_add_ln_(wave|generic)_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)fused_add_ln_(wave|generic)_kernel"
 
     def __init__(
         self,

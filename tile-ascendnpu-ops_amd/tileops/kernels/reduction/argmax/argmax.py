@@ -52,7 +52,7 @@ class ArgreduceKernel(Kernel):
         device_index: Accepted for API compatibility.
     """
 
-    profile_kernel_name = r"tileops\d+row_reduce_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)row_reduce_kernel"
 
     def __init__(
         self,

@@ -47,7 +47,7 @@ class LogSumExpKernel(Kernel):
             per-device sizing).
     """
 
-    profile_kernel_name = r"tileops\d+row_reduce_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)row_reduce_kernel"
 
     def __init__(
         self,

@@ -57,7 +57,12 @@ def _analyze_performance(benchmark: dict[str, Any]) -> tuple[list[dict], dict, l
             warnings.append(f"{operator}/{case_id}: invalid tileops profile: {reason}")
         if requested == "rocprof" and mode != "rocprof":
             fallback += 1
-            warnings.append(f"{operator}/{case_id}: requested rocprof but recorded {mode or 'unknown'}")
+            why = result.get("rocprof_fallback")
+            warnings.append(f"{operator}/{case_id}: requested rocprof but recorded {mode or 'unknown'}"
+                            + (f" ({why})" if why else ""))
+        ctr_err = (result.get("rocprof") or {}).get("counters_error")
+        if ctr_err:
+            warnings.append(f"{operator}/{case_id}: counter collection failed ({ctr_err})")
         meta = result.get("rocprof") or None
         cases.append({
             "operator": operator,
@@ -76,6 +81,9 @@ def _analyze_performance(benchmark: dict[str, Any]) -> tuple[list[dict], dict, l
             "performance_tops": result.get("Perf(TOps/s)", result.get("tflops")),
             "computility_tops": result.get("Computility(TOPs/s)"),
             "bound": result.get("bound"),
+            "hbm_bytes_measured": result.get("HBM bytes (counters)"),
+            "hbm_tb_s_measured": result.get("HBM(TB/s, counters)"),
+            "mfma_busy_percent": result.get("MFMA busy(%)"),
             "kernels": [k.get("name") for k in (meta or {}).get("kernels", [])] or None,
             "rocprof": meta,
         })

@@ -36,6 +36,9 @@ def _parser() -> argparse.ArgumentParser:
     run.add_argument("--timeout", type=int, help="timeout in seconds for each pytest stage")
     run.add_argument("--pytest-arg", action="append", default=[],
                      help="additional pytest argument; repeat for several")
+    run.add_argument("--with-counters", action="store_true",
+                     help="rocprof mode: also collect HBM bytes (FETCH_SIZE / WRITE_SIZE) and "
+                          "MFMA busy per case (three more profiled runs per case)")
     render = sub.add_parser("render", help="regenerate Markdown/HTML from run.json")
     render.add_argument("run_json")
     render.add_argument("--output-dir")
@@ -69,7 +72,7 @@ def main(argv: list[str] | None = None) -> int:
         benchmark_file=args.benchmark_file, prof_mode=args.prof_mode,
         kernel_name=args.kernel_name, reports_dir=args.reports_dir,
         pytest_args=args.pytest_arg, timeout=args.timeout,
-        with_session_timing=args.with_session_timing)
+        with_session_timing=args.with_session_timing, with_counters=args.with_counters)
     print(f"[tileops-report] status={run['status']} report={run_dir / 'report.md'}")
     return code
 

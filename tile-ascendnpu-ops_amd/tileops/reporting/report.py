@@ -130,14 +130,27 @@ def _failed_cases(run: dict[str, Any]) -> list[tuple[str, dict]]:
 
 _PERF_HEAD = ("Label", "Latency (us)", "Ratio (%)", "AI (Ops/Byte)", "Bound", "Shape / Parameters",
               "DType", "Mode", "Kernels", "Bandwidth (TB/s)", "Perf (TOps/s)")
+# with rocprofv3 counters (tileops-report run --with-counters)
+_COUNTER_HEAD = ("HBM (TB/s, counters)", "HBM bytes / roofline bytes", "MFMA busy (%)")
 
 
-def _perf_row(case: dict[str, Any]) -> list[str]:
+def _has_counters(cases: list[dict[str, Any]]) -> bool:
+    return any(c.get("hbm_bytes_measured") is not None for c in cases)
+
+
+def _perf_row(case: dict[str, Any], counters: bool = False) -> list[str]:
     p = case.get("params") or {}
-    return [_label(case), _fmt(case.get("latency_us")), _fmt(case.get("roofline_utilization_percent"), 2),
-            _fmt(case.get("arithmetic_intensity_ops_per_byte")), case.get("bound") or "?",
-            _shape(p), _dtype(p), case.get("prof_mode") or "N/A", _kernels(case),
-            _fmt(case.get("bandwidth_tb_s")), _fmt(case.get("performance_tops"))]
+    row = [_label(case), _fmt(case.get("latency_us")), _fmt(case.get("roofline_utilization_percent"), 2),
+           _fmt(case.get("arithmetic_intensity_ops_per_byte")), case.get("bound") or "?",
+           _shape(p), _dtype(p), case.get("prof_mode") or "N/A", _kernels(case),
+           _fmt(case.get("bandwidth_tb_s")), _fmt(case.get("performance_tops"))]
+    if counters:
+        bw, lat = case.get("bandwidth_tb_s"), case.get("latency_us")
+        roof = bw * lat * 1e6 if isinstance(bw, (int, float)) and isinstance(lat, (int, float)) else None
+        meas = case.get("hbm_bytes_measured")
+        ratio = meas / roof if meas is not None and roof else None
+        row += [_fmt(case.get("hbm_tb_s_measured")), _fmt(ratio, 3), _fmt(case.get("mfma_busy_percent"), 1)]
+    return row
 
 
 def _timing(run: dict[str, Any]) -> list[tuple[str, dict]]:
@@ -184,14 +197,20 @@ def render_markdown(run: dict[str, Any]) -> str:
               "over measured latency per shape, against MI355X peaks (HBM 8 TB/s; MFMA "
               "2516.6 TFLOP/s fp16/bf16; 157.3 TFLOP/s fp32).", "", "## Operator Details", ""]
     perf = run["performance"].get("cases", [])
+    counters = _has_counters(perf)
+    head = _PERF_HEAD + (_COUNTER_HEAD if counters else ())
+    if counters:
+        lines += ["> Counters (rocprofv3): HBM bytes per call from FETCH_SIZE / WRITE_SIZE scaled "
+                  "by a device-copy calibration, and their ratio to the roofline bytes; MFMA busy "
+                  "= SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM_GUI_ACTIVE / 8).", ""]
     for op in run["operators"]:
         name = op.get("operator")
         cases = [c for c in perf if c.get("operator") == name]
-        lines += [f"### {name}", "", "| " + " | ".join(_PERF_HEAD) + " |",
-                  "|---|---:|---:|---:|:---:|---|---|---|---|---:|---:|"]
-        lines += ["| " + " | ".join(_cell(x) for x in _perf_row(c)) + " |" for c in cases]
+        lines += [f"### {name}", "", "| " + " | ".join(head) + " |",
+                  "|---|---:|---:|---:|:---:|---|---|---|---|---:|---:|" + ("---:|" * 3 if counters else "")]
+        lines += ["| " + " | ".join(_cell(x) for x in _perf_row(c, counters)) + " |" for c in cases]
         if not cases:
-            lines.append("| - | No performance records |" + " - |" * (len(_PERF_HEAD) - 2))
+            lines.append("| - | No performance records |" + " - |" * (len(head) - 2))
         lines.append("")
     timing = _timing(run)
     if timing:
@@ -256,10 +275,13 @@ def render_html(run: dict[str, Any]) -> str:
                          for op in run["operators"]], {1, 2, 3, 4}))
     parts.append("<h2>Operator Details</h2>")
     perf = run["performance"].get("cases", [])
+    counters = _has_counters(perf)
+    head = list(_PERF_HEAD + (_COUNTER_HEAD if counters else ()))
+    numeric = {1, 2, 3, 9, 10} | ({11, 12, 13} if counters else set())
     for op in run["operators"]:
         cases = [c for c in perf if c.get("operator") == op.get("operator")]
         parts.append(f"<h3>{html.escape(str(op.get('operator')))}</h3>")
-        parts.append(_table(list(_PERF_HEAD), [_perf_row(c) for c in cases], {1, 2, 3, 9, 10})
+        parts.append(_table(head, [_perf_row(c, counters) for c in cases], numeric)
                      if cases else "<p>No performance records.</p>")
     timing = _timing(run)
     if timing:

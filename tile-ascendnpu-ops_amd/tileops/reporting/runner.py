@@ -180,6 +180,7 @@ def run_operator(
     timeout: int | None = None,
     root: str | Path | None = None,
     with_session_timing: bool = False,
+    with_counters: bool = False,
 ) -> tuple[dict[str, Any], Path, int]:
     """Run one operator (or ``all``) and write its report directory.
 
@@ -225,6 +226,10 @@ def run_operator(
             benv["TILEOPS_ROCPROF_KERNEL_NAME"] = kernel_name
         else:
             benv.pop("TILEOPS_ROCPROF_KERNEL_NAME", None)
+        if with_counters and prof_mode == "rocprof":
+            benv["TILEOPS_ROCPROF_COUNTERS"] = "1"
+        else:
+            benv.pop("TILEOPS_ROCPROF_COUNTERS", None)
         print(f"[tileops-report] benchmark: {bench_target} ({prof_mode})", flush=True)
         bench_xml = pytest_dir / "benchmark.xml"
         bench_code, bench_cmd = _run_pytest(
