@@ -35,7 +35,12 @@ SHAPES = [
     pytest.param(1025, 4096, torch.float16, marks=pytest.mark.full),
     pytest.param(16, 1152, torch.float16, marks=pytest.mark.smoke),
     pytest.param(8, 8192, torch.bfloat16, marks=pytest.mark.full),
-    pytest.param(4, 16384, torch.bfloat16, marks=pytest.mark.full),  # beyond registers
+    # one workgroup per row, 5..8 packs per lane (1024 < N / pack <= 2048)
+    pytest.param(4, 16384, torch.bfloat16, marks=pytest.mark.full),
+    pytest.param(7, 8192, torch.float32, marks=pytest.mark.full),
+    pytest.param(9, 12288, torch.float16, marks=pytest.mark.full),
+    pytest.param(3, 6148, torch.float32, marks=pytest.mark.full),  # last pack column: 1 lane
+    pytest.param(2, 32768, torch.bfloat16, marks=pytest.mark.full),  # beyond registers
     pytest.param(5, 1001, torch.float16, marks=pytest.mark.full),  # odd N: generic path
 ]
 
@@ -68,15 +73,16 @@ def test_fused_add_layer_norm_many_rows(param_dtype):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_fused_add_layer_norm_fp32_params(dtype):
-    test = FusedAddLayerNormTest(256, 4096, dtype, param_dtype=torch.float32)
+@pytest.mark.parametrize("n", [4096, 13312])  # wavefront-per-row, workgroup-per-row
+def test_fused_add_layer_norm_fp32_params(dtype, n):
+    test = FusedAddLayerNormTest(256, n, dtype, param_dtype=torch.float32)
     x, r, w, b = test.gen_inputs()
     assert w.dtype == torch.float32
     op = FusedAddLayerNormFwdOp(dtype=dtype)
     atol, rtol = ref_tolerance(dtype)
     test.check(op, x, r, w, b, atol=atol, rtol=rtol)
     flops, nbytes = op.eval_roofline()
-    assert nbytes == 4 * 256 * 4096 * 2 + 2 * 4096 * 4
+    assert nbytes == 4 * 256 * n * 2 + 2 * n * 4
 
 
 @pytest.mark.gpu

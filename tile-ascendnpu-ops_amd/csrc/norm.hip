@@ -10,7 +10,10 @@
 // lane): one wavefront per row, the two row statistics are wavefront
 // butterflies, w / b are staged once per workgroup into LDS as fp32 so that
 // the HBM stream is only x, residual in and y, r_out out.
-// Fallback: one workgroup per row, three passes over global memory.
+// Long rows (up to 32 packs per lane of a wavefront): one 256-lane
+// workgroup per row, the row in registers, workgroup reductions.
+// Fallback (any N or alignment): grid-stride workgroups, three passes over
+// global memory.
 #include "common.h"
 
 namespace tileops {
@@ -174,6 +177,117 @@ __global__ __launch_bounds__(WPB * 64) void fused_add_ln_wave_kernel(
   }
 }
 
+// w[i..i+V) and b[i..i+V) as fp32: 16-byte loads when both are 16-byte
+// aligned and N is a multiple of their pack (V is a multiple of it, since W
+// is never narrower than T), else element loads.
+template <typename T, typename W>
+__device__ __forceinline__ void load_params(const W* w, const W* b, int64_t i, bool vec,
+                                            float (&wv)[Elem<T>::kVec],
+                                            float (&bv)[Elem<T>::kVec]) {
+  constexpr int V = Elem<T>::kVec;
+  constexpr int PV = 16 / sizeof(W);
+  if (vec) {
+#pragma unroll
+    for (int j = 0; j < V; j += PV) {
+      const Pack<W> w4 = *reinterpret_cast<const Pack<W>*>(w + i + j);
+      const Pack<W> b4 = *reinterpret_cast<const Pack<W>*>(b + i + j);
+#pragma unroll
+      for (int e = 0; e < PV; ++e) {
+        wv[j + e] = Elem<W>::to_f32(w4.v[e]);
+        bv[j + e] = Elem<W>::to_f32(b4.v[e]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      wv[e] = wload(w, i + e);
+      bv[e] = wload(b, i + e);
+    }
+  }
+}
+
+// Sum of v over the 256-lane workgroup (four wavefronts); every lane gets it.
+__device__ __forceinline__ float block_sum4(float v, float* part) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float t = (part[0] + part[1]) + (part[2] + part[3]);
+  __syncthreads();
+  return t;
+}
+
+// Long rows (1024 < packs <= 2048: fp32 N <= 8192, 16-bit N <= 16384): one
+// 256-lane workgroup per row, KP packs per lane held in registers, so the
+// rounded sum is never re-read from memory (the three-pass kernel re-reads
+// r_out twice, and at thousands of rows in flight those re-reads miss L2).
+// w / b come straight from global memory (L2-resident across rows).
+template <typename T, typename W, int KP>
+__global__ __launch_bounds__(256) void fused_add_ln_block_kernel(
+    const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
+    const W* __restrict__ b, T* __restrict__ y, T* __restrict__ rout, int N, float eps,
+    bool vec_params) {
+  constexpr int V = Elem<T>::kVec;
+  __shared__ float part[4];
+  const int npack = N / V;
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * N;
+  const T* rr = res + row * N;
+  // every lane loads all KP packs, past-the-end ones clamped onto the row's
+  // last pack (one uniform load sequence); they are masked out below
+  Pack<T> xs[KP], rs[KP];
+#pragma unroll
+  for (int k = 0; k < KP; ++k) {
+    const int p = min(k * 256 + (int)threadIdx.x, npack - 1);
+    xs[k] = load_pack_nt(xr + (int64_t)p * V);
+    rs[k] = load_pack_nt(rr + (int64_t)p * V);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KP; ++k) {
+    const int p = k * 256 + threadIdx.x;
+    float s_part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const T s = Elem<T>::from_f32(Elem<T>::to_f32(xs[k].v[e]) + Elem<T>::to_f32(rs[k].v[e]));
+      xs[k].v[e] = s;
+      s_part += Elem<T>::to_f32(s);
+    }
+    if (p < npack) {
+      sum += s_part;
+      store_pack_nt(rout + row * N + (int64_t)p * V, xs[k]);
+    }
+  }
+  const float inv_n = 1.0f / (float)N;
+  const float mean = block_sum4(sum, part) * inv_n;
+  float sq = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KP; ++k) {
+    float q_part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
+      q_part = fmaf(d, d, q_part);
+    }
+    if (k * 256 + (int)threadIdx.x < npack) sq += q_part;
+  }
+  const float rstd = 1.0f / sqrtf(block_sum4(sq, part) * inv_n + eps);
+#pragma unroll
+  for (int k = 0; k < KP; ++k) {
+    const int p = k * 256 + threadIdx.x;
+    if (p < npack) {
+      float wv[V], bv[V];
+      load_params<T, W>(w, b, (int64_t)p * V, vec_params, wv, bv);
+      Pack<T> o;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const float d = Elem<T>::to_f32(xs[k].v[e]) - mean;
+        o.v[e] = Elem<T>::from_f32(fmaf(d * rstd, wv[e], bv[e]));
+      }
+      store_pack_nt(y + row * N + (int64_t)p * V, o);
+    }
+  }
+}
+
 // General rows: any N, any alignment.  Pass 1 writes r_out and sums it,
 // pass 2 re-reads r_out (L2-resident for one row) for the variance, pass 3
 // normalises.
@@ -244,13 +358,25 @@ static int launch_fused_add_ln(const void* xv, const void* rv, const void* wv, c
   const bool packable = N % V == 0 && host_aligned16(x) && host_aligned16(r) &&
                         host_aligned16(y) && host_aligned16(ro);
   const int64_t lane_packs = (N / V + 63) / 64;
-  if (packable && lane_packs <= 16 && M <= (int64_t)UINT32_MAX) {
+  // grid x dimension times block size stays within 32 bits on both fast paths
+  if (packable && lane_packs <= 16 && M <= (int64_t)(UINT32_MAX / 64)) {
     const int n = (int)N;
     if (lane_packs <= 1) launch_wave<T, W, 1>(x, r, w, b, y, ro, M, n, eps, s);
     else if (lane_packs <= 2) launch_wave<T, W, 2>(x, r, w, b, y, ro, M, n, eps, s);
     else if (lane_packs <= 4) launch_wave<T, W, 4>(x, r, w, b, y, ro, M, n, eps, s);
     else if (lane_packs <= 8) launch_wave<T, W, 8>(x, r, w, b, y, ro, M, n, eps, s);
     else launch_wave<T, W, 16>(x, r, w, b, y, ro, M, n, eps, s);
+  } else if (packable && lane_packs <= 32 && M <= (int64_t)(UINT32_MAX / 256)) {
+    // 1024 < N / V <= 2048: KP = ceil(packs / 256) in 5..8
+    const int n = (int)N;
+    const int kp = (int)((N / V + 255) / 256);
+    constexpr int PV = 16 / (int)sizeof(W);
+    const bool vec = N % PV == 0 && host_aligned16(w) && host_aligned16(b);
+    const dim3 grid((unsigned)M), block(256);
+    if (kp <= 5) fused_add_ln_block_kernel<T, W, 5><<<grid, block, 0, s>>>(x, r, w, b, y, ro, n, eps, vec);
+    else if (kp == 6) fused_add_ln_block_kernel<T, W, 6><<<grid, block, 0, s>>>(x, r, w, b, y, ro, n, eps, vec);
+    else if (kp == 7) fused_add_ln_block_kernel<T, W, 7><<<grid, block, 0, s>>>(x, r, w, b, y, ro, n, eps, vec);
+    else fused_add_ln_block_kernel<T, W, 8><<<grid, block, 0, s>>>(x, r, w, b, y, ro, n, eps, vec);
   } else {
     int64_t blocks = M < 256 * 16 ? M : 256 * 16;
     fused_add_ln_generic_kernel<T, W><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(x, r, w, b, y,

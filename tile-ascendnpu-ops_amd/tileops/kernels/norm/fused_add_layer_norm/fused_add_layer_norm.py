@@ -10,8 +10,10 @@ Per row of N elements::
 with mean / biased variance of the rounded sum in fp32.  ``forward`` returns a
 list ``[y, residual_out]`` shaped like ``x``.  ``weight`` / ``bias`` may be the
 input dtype (the reference contract) or float32.
-Device code: fused_add_ln_wave_kernel (N a multiple of 8 up to 8192) and
-fused_add_ln_generic_kernel in csrc/norm.hip.
+Device code (csrc/norm.hip): fused_add_ln_wave_kernel (up to 1024 16-byte
+packs per row: one wavefront per row), fused_add_ln_block_kernel (1025 to
+2048 packs: one 256-lane workgroup per row, the row in registers) and
+fused_add_ln_generic_kernel (any other N or alignment).
 """
 
 from typing import Optional
@@ -36,7 +38,7 @@ class FusedAddLayerNormKernel(Kernel):
     """
 
     SUPPORTED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
-    profile_kernel_name = r"tileops(?:::|\d+)fused_add_ln_(wave|generic)_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)fused_add_ln_(wave|block|generic)_kernel"
 
     def __init__(
         self,
@@ -62,7 +64,7 @@ class FusedAddLayerNormKernel(Kernel):
     def default_config(self) -> dict:
         # fused_add_ln_wave_kernel: one wavefront per row with the row held in
         # registers, four rows per 256-thread workgroup, weight / bias staged
-        # in LDS as fp32
+        # in LDS as fp32 (longer rows: one 256-thread workgroup per row)
         return {"rows_per_wave": 1, "rows_per_workgroup": 4}
 
     def forward(
