@@ -123,14 +123,13 @@ __device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d)
 constexpr int AS = 72;  // fp32 row stride of A^T / T (288 bytes: float4-aligned rows)
 constexpr int XS = 36;  // fp32 row stride of X
 
-// Global operands of one chunk for one thread, loaded a chunk ahead: k rows
-// 4vg..4vg+3 (dims 8vc..8vc+7), g / beta of token `lane`, and the q row this
-// wavefront's Q K^T block needs, in the MFMA B layout.  One uniform sequence
-// for every wavefront (wave 3 loads q rows it does not use); rows past T load
-// the chunk's last row and are zeroed where they are consumed.
+// Global operands of one chunk for one thread, loaded a chunk ahead: 16
+// bytes (dims 8 (tid & 15) ..) of k and q rows 16 i + tid / 16 (i < 4), so
+// that every load instruction reads four whole 256-byte rows, and g / beta
+// of token `lane`.  Rows past T load the chunk's last row and are zeroed
+// where they are staged.
 struct PrepLoads {
-  u32x4 kr[4];
-  bf16x8 aq[DK / 16];
+  u32x4 kr[4], qr[4];
   float g, beta;
 };
 
@@ -142,6 +141,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(16))) float r1[C * AS];
   __shared__ __attribute__((aligned(16))) float x_s[32 * XS];
   __shared__ __attribute__((aligned(16))) float gc_s[C], beta_s[C];
+  __shared__ __attribute__((aligned(16))) bf16 q_s[C * KP];
   static_assert(C * KP * 2 <= C * AS * 4, "k tile must fit the T region");
   bf16* k_s = reinterpret_cast<bf16*>(r0);
   float* t_s = r0;
@@ -151,8 +151,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int col = lane & 31, half = lane >> 5;
   const int rb = wave == 0 ? 0 : 1;  // Q K^T / K K^T block of waves 0-2
   const int cb = wave == 2 ? 1 : 0;
-  const int qrow = rb * 32 + col;
-  const int vg = tid & 15, vc = tid >> 4;
+  const int lrow = tid >> 4, lchk = tid & 15;  // row (of 16) and 16-byte chunk of the loads
   const int64_t tok_stride = (int64_t)H * DK;  // DK == DV
   // record blk of the workspace: (b, h) = blk / NS, chunk c0 + blk % NS
   const uint64_t nblk = (uint64_t)B * H * NS;
@@ -161,23 +160,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int chunk = c0 + (int)(blk % NS), bh = (int)(blk / NS);
     const int h = bh % H, b = bh / H;
     const int t0 = chunk * C, n = min(C, T - t0);
-    const bf16* kb = k + ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK + vc * 8;
+    const int64_t off0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK + lchk * 8;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      L.kr[i] = *reinterpret_cast<const u32x4*>(kb + min(4 * vg + i, n - 1) * tok_stride);
+    for (int i = 0; i < 4; ++i) {
+      const int64_t off = off0 + (int64_t)min(16 * i + lrow, n - 1) * tok_stride;
+      L.kr[i] = *reinterpret_cast<const u32x4*>(k + off);
+      L.qr[i] = *reinterpret_cast<const u32x4*>(q + off);
+    }
     const int64_t gi = ((int64_t)b * T + t0 + min(lane, n - 1)) * H + h;
     L.g = g[gi];
     L.beta = beta[gi];
-    const bf16* qp = q + ((int64_t)b * T + t0 + min(qrow, n - 1)) * tok_stride + (int64_t)h * DK;
-#pragma unroll
-    for (int ks = 0; ks < DK / 16; ++ks) L.aq[ks] = ld8(qp + ks * 16 + half * 8);
   };
 
   // Persistent: workgroup i takes chunks i, i + grid, ...; the next chunk's
   // loads are issued as soon as the current one's registers are consumed.
   PrepLoads cur;
+  // (see the settle before the record stores below; here for the first
+  // chunk's loads, so that both paths into the loop arrive settled)
+  auto settle = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(cur.kr[i]), "+v"(cur.qr[i]));
+    asm volatile("" : "+v"(cur.g), "+v"(cur.beta));
+  };
   uint64_t blk = blockIdx.x;
   if (blk < nblk) load(blk, cur);
+  settle();
   for (; blk < nblk; blk += gridDim.x) {
     const int chunk = c0 + (int)(blk % NS);
     const int t0 = chunk * C;
@@ -187,12 +194,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     bf16* aqk_ws = reinterpret_cast<bf16*>(wsc + kAqkOff);
     float* fac_ws = reinterpret_cast<float*>(wsc + kFacOff);
 
-    // ---- stage k; rows past T are 0
+    // ---- stage k and q; rows past T are 0
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = 4 * vg + i;
-      if (row >= n) cur.kr[i] = u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(k_s + row * KP + vc * 8) = cur.kr[i];
+      const int row = 16 * i + lrow;
+      if (row >= n) cur.kr[i] = cur.qr[i] = u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(k_s + row * KP + lchk * 8) = cur.kr[i];
+      *reinterpret_cast<u32x4*>(q_s + row * KP + lchk * 8) = cur.qr[i];
     }
     if (wave == 3) {
       float x = lane < n ? cur.g : 0.0f;
@@ -221,12 +229,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // rows l of block rb as B, so that a lane owns one row l (column of the
       // result) and its 16 values run over s: [s][l] = k_s . k_l and k_s . q_l
       f32x16 kk = {}, qk = {};
-      const bool qlive = qrow < n;
 #pragma unroll
       for (int ks = 0; ks < DK / 16; ++ks) {
         const bf16x8 bs = ld8(k_s + (cb * 32 + col) * KP + ks * 16 + half * 8);
         const bf16x8 bl = ld8(k_s + (rb * 32 + col) * KP + ks * 16 + half * 8);
-        const bf16x8 a = qlive ? cur.aq[ks] : bf16x8{};
+        const bf16x8 a = ld8(q_s + (rb * 32 + col) * KP + ks * 16 + half * 8);
         kk = mfma(bs, bl, kk);
         qk = mfma(bs, a, qk);
       }
@@ -354,6 +361,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int r = 0; r < 4; ++r) t_s[(32 + 16 * qi + 4 * mk + r) * AS + 16 * qj + mi] = -y[r];
     }
     lds_barrier();
+
+    // The next chunk's operands (loaded after the products above) pass
+    // through an empty asm before the record stores below: the compiler
+    // resolves their loads here, while only older stores are in flight.
+    // Otherwise its bookkeeping across the loop places those waits at their
+    // first use, after these stores, and waits for the stores as well.
+    settle();
 
     // ---- Tu = T diag(beta) in bf16 to the record (T12 is zero); 4
     // consecutive columns per thread: float4 in, one 8-byte store out
