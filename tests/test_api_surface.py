@@ -180,7 +180,10 @@ def test_config_overrides_must_match_the_compiled_kernel(capsys):
     with pytest.raises(ValueError, match="unknown config keys"):
         HardswishFwdKernel(64, torch.float16, config={"unroll": 4})
     mha = GQAPrefillFwdKernel(1, 2, 2, 256, 256, 128, True, torch.bfloat16)
-    assert mha.config["block_m"] == 256 and mha.config["num_stages"] == 3
+    assert mha.config["block_m"] == 256 and mha.config["block_n"] == 128
+    assert mha.config["num_stages"] == 2
+    mha64 = GQAPrefillFwdKernel(1, 2, 2, 256, 256, 64, True, torch.bfloat16)
+    assert mha64.config["block_n"] == 64 and mha64.config["num_stages"] == 3
     with pytest.raises(ValueError, match="block_m=128"):
         GQAPrefillFwdKernel(1, 2, 2, 256, 256, 128, True, torch.bfloat16, config={"block_m": 128})
 

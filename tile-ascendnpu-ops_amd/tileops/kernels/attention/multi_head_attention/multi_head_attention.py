@@ -113,7 +113,10 @@ class GQAPrefillFwdKernel(Kernel):
     @property
     def default_config(self) -> dict:
         # mha_fwd_kernel: 256 query rows per 512-thread workgroup (8
-        # wavefronts x 32 rows), 64-key K / V tiles in three LDS slots
+        # wavefronts x 32 rows); head dim 128: 128-key K / V tiles in two LDS
+        # slots each; head dims 64 and 256: 64-key tiles in three slots
+        if self.dim == 128:
+            return {"block_m": 256, "block_n": 128, "num_stages": 2, "threads": 512}
         return {"block_m": 256, "block_n": 64, "num_stages": 3, "threads": 512}
 
     def forward(
