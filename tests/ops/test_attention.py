@@ -71,6 +71,8 @@ def _sample_pairs(B, H, n=6, seed=0):
                      id="manifest-smoke-causal-fp16"),
         pytest.param(2, 1000, 4, 128, True, torch.bfloat16, marks=pytest.mark.full,
                      id="ragged-causal"),
+        pytest.param(2, 1000, 4, 128, False, torch.bfloat16, marks=pytest.mark.full,
+                     id="ragged-noncausal"),
         pytest.param(3, 77, 2, 64, False, torch.float16, marks=pytest.mark.full,
                      id="tiny-ragged"),
     ],
