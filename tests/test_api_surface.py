@@ -102,7 +102,8 @@ _MANGLED = {
              "_ZN7tileops18isfp_scalar_kernelIfLi1EEEvPKT_Phll"],
     "gated": ["_ZN7tileops21gated_gelu_vec_kernelIDF16b_Li0ELi2EEEvPKT_PS1_ll",
               "_ZN7tileops24gated_gelu_scalar_kernelIfLi1EEEvPKT_PS1_ll",
-              "void tileops::gated_gelu_vec_kernel<float, 0, 2>(float const*, float*, long, long)"],
+              "void tileops::gated_gelu_vec_kernel<float, 0>(float const*, float*, unsigned int, unsigned int)",
+              "_ZN7tileops22gated_gelu_rows_kernelIDF16b_Li1ELi2EEEvPKT_PS1_ll"],
     "bcast": ["_ZN7tileops16bcast_vec_kernelIfLi0EEEvPKT_S3_S3_PS1_lf",
               "_ZN7tileops18bcast_inner_kernelIDF16_Li1EjEEvPKT_S3_S3_PS1_T1_S5_f",
               "_ZN7tileops16bcast_any_kernelIfLi2EEEvPKT_S3_S3_PS1_llfNS_9BcastDescE"],

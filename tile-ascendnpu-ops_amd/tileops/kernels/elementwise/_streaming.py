@@ -128,7 +128,7 @@ class GatedGeluFwdKernel(Kernel):
 
     SUPPORTED_DTYPES = _FLOAT_DTYPES
     _approx: int = 0
-    profile_kernel_name = r"tileops(?:::|\d+)gated_gelu_(vec|scalar)_kernel"
+    profile_kernel_name = r"tileops(?:::|\d+)gated_gelu_(vec|rows|scalar)_kernel"
 
     def __init__(self, M: int, N: int, dtype: torch.dtype, config: Optional[dict] = None):
         super().__init__()
@@ -141,9 +141,10 @@ class GatedGeluFwdKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # gated_gelu_vec_kernel: grid (column blocks, rows), 256-thread
-        # workgroups, two 16-byte gate packs and two value packs per thread
-        return {"threads": 256, "vector_bytes": 16, "packs_per_thread": 2}
+        # gated_gelu_vec_kernel: one-shot grid of 256-thread workgroups over
+        # the flattened output, one 16-byte gate pack, one value pack and
+        # one output pack per thread
+        return {"threads": 256, "vector_bytes": 16, "packs_per_thread": 1}
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         _native.require_device(x)
