@@ -318,7 +318,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int r = 0; r < 4; ++r) x_s[(16 * wave + 4 * mk + r) * XS + mi] = y[r];
     }
-    lds_barrier();
+    // no barrier: each of waves 0, 1 reads back only its own Y rows, T11 /
+    // T33 are settled since the substitution's barrier, and the zero blocks
+    // written below are read by no wavefront before the next barrier
     if (wave < 2) {  // T10 = -T11 Y (wave 0), T32 = -T33 Y (wave 1)
       const int d0 = 32 * wave;
       f32x4 z = {};
