@@ -71,3 +71,20 @@ def test_noalloc_rejects_heads_beyond_the_array():
     code = lib.tileops_gdn_prefill_fwd_noalloc(fake, fake, fake, fake, fake, None, fake, fake,
                                                1, 64, H, 128, 128, 64, 0.1, BF16, None)
     assert code == -4  # TILEOPS_EWORKSPACE
+
+
+@pytest.mark.gpu
+def test_noalloc_zero_length_passes_the_state_through_for_any_head_count():
+    # with T = 0 there are no chunks and no scratch is used, so the head
+    # count that the array bounds for T > 0 must not be rejected
+    lib = _native.lib()
+    B, H = 1, SCRATCH_BYTES // RECORD_BYTES + 1
+    h0 = torch.randn(B, H, 128, 128, device="cuda")
+    hT = torch.full_like(h0, float("nan"))
+    e = torch.empty(B, 0, H, 128, device="cuda", dtype=torch.bfloat16)
+    z = torch.empty(B, 0, H, device="cuda")
+    code = lib.tileops_gdn_prefill_fwd_noalloc(*_args(e, e, e, z, z, h0, e, hT, B, 0, H),
+                                               _native.stream_of(h0))
+    _native.check(code, "tileops_gdn_prefill_fwd_noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(hT, h0)

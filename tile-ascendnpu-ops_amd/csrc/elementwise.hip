@@ -69,9 +69,10 @@ __device__ __forceinline__ float unary_op(float x, float lo, float hi, int flags
 // non-temporal pack per thread with a grid covering the whole tensor streams
 // a read+write workload at ~82% of HBM peak, ahead of grid-stride loops
 // (~65%) and of several packs per thread (~75%).
+// x and y may be the same buffer (the Ops' in-place path): every thread
+// reads its pack before it writes it, so neither pointer is __restrict__.
 template <typename T, int OP>
-__global__ __launch_bounds__(256) void unary_vec_kernel(const T* __restrict__ x,
-                                                        T* __restrict__ y, int64_t npack,
+__global__ __launch_bounds__(256) void unary_vec_kernel(const T* x, T* y, int64_t npack,
                                                         float lo, float hi, int flags) {
   constexpr int V = Elem<T>::kVec;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -86,8 +87,7 @@ __global__ __launch_bounds__(256) void unary_vec_kernel(const T* __restrict__ x,
 
 // Scalar path: tails after the packed body, and misaligned tensors.
 template <typename T, int OP>
-__global__ __launch_bounds__(256) void unary_scalar_kernel(const T* __restrict__ x,
-                                                           T* __restrict__ y, int64_t begin,
+__global__ __launch_bounds__(256) void unary_scalar_kernel(const T* x, T* y, int64_t begin,
                                                            int64_t n, float lo, float hi,
                                                            int flags) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;

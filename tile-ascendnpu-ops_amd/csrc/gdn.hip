@@ -320,7 +320,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     // no barrier: each of waves 0, 1 reads back only its own Y rows, T11 /
     // T33 are settled since the substitution's barrier, and the zero blocks
-    // written below are read by no wavefront before the next barrier
+    // written below are read by no wavefront before the next barrier.  Lanes
+    // read Y values other lanes of the same wavefront wrote: the fences keep
+    // the compiler from moving those LDS reads above the writes (the LDS
+    // operations of one wavefront execute in order, so no s_barrier is needed)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (wave < 2) {  // T10 = -T11 Y (wave 0), T32 = -T33 Y (wave 1)
       const int d0 = 32 * wave;
       f32x4 z = {};
@@ -875,7 +880,7 @@ extern "C" int tileops_gdn_prefill_fwd_noalloc(const void* q, const void* k, con
   if (int e = gdn::check_args(q, k, v, g, beta, o, hT, B, T, H, K, V, chunk, dtype)) return e;
   if (B == 0) return 0;
   const int64_t per_chunk = B * H * (int64_t)gdn::kChunkBytes;  // one chunk of every head
-  if (per_chunk > (int64_t)gdn::kScratchBytes) return TILEOPS_EWORKSPACE;
+  if (T > 0 && per_chunk > (int64_t)gdn::kScratchBytes) return TILEOPS_EWORKSPACE;
   uint8_t* ws = nullptr;
   if (int e = gdn::scratch_ptr(&ws)) return e;
   const int nc = (int)((T + gdn::C - 1) / gdn::C);
