@@ -211,7 +211,8 @@ int tileops_mha_fwd(const void* q, const void* k, const void* v, void* o, float*
  * g is the log-decay)   h0: [B, H, K, V] F32 or NULL (zero state)
  * o: [B, T, H, V] BF16   hT: [B, H, K, V] F32 (final state).
  * K and V must be 128; chunk must be 64.  `ws` is a device workspace of at
- * least tileops_gdn_prefill_workspace_bytes(...) bytes.
+ * least tileops_gdn_prefill_workspace_bytes(...) bytes (0 when the sequence
+ * runs as one segment; `ws` may then be NULL).
  * No reference kernel exists (GatedDeltaNetPrefillFwdOp was not delivered,
  * MIGRATION_INDEX.md:28); the recurrence follows golden_gdn_sequential
  * (examples/gdn_prefill/probe/gdn_prefill_probe.py:60-77) and the chunked
@@ -227,16 +228,40 @@ size_t tileops_gdn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t H, int6
                                            int64_t V, int64_t chunk);
 
 /*
+ * tileops_gdn_prefill_fwd with the number of sequence segments chosen by
+ * the caller (0: the library's choice, as tileops_gdn_prefill_fwd; 1 .. 16:
+ * that many, at most one per chunk).  Segments run in parallel, each with
+ * its own state map; the workspace holds the maps
+ * (tileops_gdn_prefill_workspace_bytes_ex with the same `segments`).
+ * Same interface origin as tileops_gdn_prefill_fwd; the segment count is a
+ * scheduling knob of this implementation (the reference's
+ * GatedDeltaNetPrefillFwdOp plan names only chunk_size).
+ */
+int tileops_gdn_prefill_fwd_ex(const void* q, const void* k, const void* v,
+                               const float* g, const float* beta, const float* h0,
+                               void* o, float* hT, int64_t B, int64_t T, int64_t H,
+                               int64_t K, int64_t V, int64_t chunk, float scale,
+                               int dtype, int64_t segments, void* ws, size_t ws_bytes,
+                               void* stream);
+
+size_t tileops_gdn_prefill_workspace_bytes_ex(int64_t B, int64_t T, int64_t H, int64_t K,
+                                              int64_t V, int64_t chunk, int64_t segments);
+
+/*
  * tileops_gdn_prefill_fwd without a workspace argument, for callers that
  * cannot allocate device memory (code under stream capture, serving loops,
  * harnesses that forbid allocation): it allocates nothing and calls no
- * allocating routine.  No counterpart in the reference.  The per-chunk
- * records live in a 16 MiB device array of the library (one per GPU, held
- * until the process ends), filled segment by segment, so any T works and
- * B * H is limited to 963 (one 17 KiB record per head must fit; larger
- * B * H returns TILEOPS_EWORKSPACE).  Every call on a GPU shares that
- * array: calls that overlap on one GPU (concurrent streams, threads) race.
- * Results equal tileops_gdn_prefill_fwd's bit for bit.
+ * allocating routine.  No counterpart in the reference.  The segment maps
+ * live in a 32 MiB device array of the library (one per GPU, held until
+ * the process ends): a call uses as many segments N as the array holds
+ * (B * H * (2 N - 3) maps of 64 KiB), down to one segment, which needs no
+ * array, so every B, T and H is accepted.  Calls that use the array run one
+ * after another on the device: each waits for the previous such call's
+ * completion event, whatever stream it ran on (once per device, at the
+ * first call, the library creates that event and looks up the array's
+ * address).  Under stream capture the event is not used, and captured calls
+ * on parallel branches of one graph race on the array.  Results equal
+ * tileops_gdn_prefill_fwd_ex's with the same segment count bit for bit.
  */
 int tileops_gdn_prefill_fwd_noalloc(const void* q, const void* k, const void* v,
                                     const float* g, const float* beta, const float* h0,

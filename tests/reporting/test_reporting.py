@@ -365,18 +365,18 @@ def test_counter_totals_from_a_pmc_database(tmp_path):
     con = sqlite3.connect(db)
     con.execute("create table counters_collection (kernel_name text, counter_name text, value real)")
     con.executemany("insert into counters_collection values (?, ?, ?)", [
-        ("tileops::gdn::gdn_prep_kernel(...)", "FETCH_SIZE", 100.0),
-        ("tileops::gdn::gdn_recur_kernel(...)", "FETCH_SIZE", 50.0),
-        ("tileops::gdn::gdn_prep_kernel(...)", "FETCH_SIZE", 100.0),
+        ("void tileops::gdn::gdn_fused_kernel<8>(tileops::gdn::Args)", "FETCH_SIZE", 100.0),
+        ("void tileops::gdn::gdn_fused_kernel<4>(tileops::gdn::Args)", "FETCH_SIZE", 50.0),
+        ("void tileops::gdn::gdn_fused_kernel<8>(tileops::gdn::Args)", "FETCH_SIZE", 100.0),
         ("void at::native::copy_kernel", "FETCH_SIZE", 999.0),
-        ("tileops::gdn::gdn_recur_kernel(...)", "GRBM_GUI_ACTIVE", 8000.0),
+        ("void tileops::gdn::gdn_fused_kernel<4>(tileops::gdn::Args)", "GRBM_GUI_ACTIVE", 8000.0),
     ])
     con.commit()
     con.close()
     tot = rp.read_counter_totals(str(db), "tileops")
     assert tot == {"FETCH_SIZE": 250.0, "GRBM_GUI_ACTIVE": 8000.0}
-    assert rp.read_counter_totals(str(db), "gdn_recur") == {"FETCH_SIZE": 50.0,
-                                                           "GRBM_GUI_ACTIVE": 8000.0}
+    assert rp.read_counter_totals(str(db), "gdn_fused_kernel<4>") == {"FETCH_SIZE": 50.0,
+                                                                     "GRBM_GUI_ACTIVE": 8000.0}
 
 
 def test_profile_attaches_counters_when_asked(monkeypatch):
@@ -463,8 +463,9 @@ def test_declared_kernel_regexes_match_mangled_and_demangled_names():
     from tileops.kernels.linear_attention.gdn_prefill.gdn_prefill import GDNPrefillFwdKernel
 
     gdn = re.compile(GDNPrefillFwdKernel.profile_kernel_name)
-    assert gdn.search("tileops::gdn::gdn_recur_kernel(bool _Accum const*, _S, _P)")
-    assert gdn.search("_ZN7tileops3gdn15gdn_prep_kernelEPKDF16bS3_")
+    assert gdn.search("void tileops::gdn::gdn_fused_kernel<4>(tileops::gdn::Args)")
+    assert gdn.search("_ZN7tileops3gdn16gdn_fused_kernelILi8EEEvNS0_4ArgsE")
+    assert gdn.search("_ZN7tileops3gdn21gdn_copy_state_kernelEPKfPfl")
     mha = re.compile(GQAPrefillFwdKernel.profile_kernel_name)
     assert mha.search("_ZN7tileops3mha14mha_fwd_kernelIDF16_Li64ELi64ELb1ELi64ELb0EEEvPKT_")
     assert mha.search("void tileops::mha::mha_fwd_kernel<float, 64>(float const*)")

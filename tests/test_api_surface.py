@@ -116,9 +116,10 @@ _MANGLED = {
     "row": ["_ZN7tileops17row_reduce_kernelIfLi0ELi1ELi4ELb1EEEvPKT_Pvll",
             "void tileops::row_reduce_kernel<float, 0, 1, 4, true>(float const*, void*, long, long)"],
     "mha": ["_ZN7tileops3mha14mha_fwd_kernelIDF16b_Li128ELb1ELi64ELb0EEEvPKT_S4_S4_PS2_Pfiiiiififf"],
-    "gdn": ["_ZN7tileops3gdn15gdn_prep_kernelEPKDF16bS2_PKfS4_Phiiiif",
-            "_ZN7tileops3gdn16gdn_recur_kernelEPKDF16bPKhS2_PS0_PfS7_iiii",
-            "tileops::gdn::gdn_recur_kernel(bool _Accum const*, _S, _P, float const)"],
+    "gdn": ["_ZN7tileops3gdn16gdn_fused_kernelILi4EEEvNS0_4ArgsE",
+            "_ZN7tileops3gdn16gdn_fused_kernelILi8EEEvNS0_4ArgsE",
+            "void tileops::gdn::gdn_fused_kernel<8>(tileops::gdn::Args)",
+            "_ZN7tileops3gdn21gdn_copy_state_kernelEPKfPfl"],
     "gla": ["_ZN7tileops3gla17gla_decode_kernelIDF16bLb1EEEvPKT_S4_S4_S4_PKfPS2_Pfiiif"],
 }
 

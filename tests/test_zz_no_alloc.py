@@ -2,12 +2,13 @@
 against tileops_gdn_prefill_fwd, both called through the C ABI.
 
 The two entry points run the same kernels; the allocation-free one keeps the
-chunk records in the library's fixed device array and so works through long
-sequences in segments, carrying the state between them.  Its results must
-equal the workspace entry point's bit for bit: on two calls in a row (the
-second with a smaller input), the first long enough to take several
-segments and starting from a given state.  A call whose heads cannot fit
-the array is rejected before any launch.
+segment maps in the library's fixed device array.  Its results must equal
+the workspace entry point's bit for bit (same segment plan): on two calls in
+a row (the second with a smaller input), the first long enough to take
+several segments and starting from a given state; on two calls issued on two
+different streams one right after the other (the library orders them, since
+both use the array); and for a head count so large that the sequence runs
+as one segment, which needs no array.
 """
 
 import pytest
@@ -17,8 +18,6 @@ from tileops import _native
 from tileops.workloads.linear_attention import GdnPrefillWorkload
 
 BF16 = _native.DTYPE_CODES[torch.bfloat16]
-SCRATCH_BYTES = 16 << 20
-RECORD_BYTES = 17408
 
 
 def _args(q, k, v, g, beta, h0, o, hT, B, T, H):
@@ -27,58 +26,95 @@ def _args(q, k, v, g, beta, h0, o, hT, B, T, H):
             B, T, H, 128, 128, 64, 128**-0.5, BF16)
 
 
-def _run_both(B, T, H, with_h0):
-    lib = _native.lib()
+def _inputs(B, T, H, with_h0):
     q, k, v, g, beta = GdnPrefillWorkload(B, T, H, 128, 128).gen_inputs()
+    g = g * 0.01  # slow decay: the segment maps carry the state
     h0 = torch.randn(B, H, 128, 128, device="cuda") * 0.1 if with_h0 else None
-    stream = _native.stream_of(q)
-    o_ref = torch.empty_like(v)
-    hT_ref = torch.empty(B, H, 128, 128, device="cuda")
+    return q, k, v, g, beta, h0
+
+
+def _reference(lib, inp, B, T, H, stream):
+    q, k, v, g, beta, h0 = inp
+    o = torch.empty_like(v)
+    hT = torch.empty(B, H, 128, 128, device="cuda")
     need = lib.tileops_gdn_prefill_workspace_bytes(B, T, H, 128, 128, 64)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
-    code = lib.tileops_gdn_prefill_fwd(*_args(q, k, v, g, beta, h0, o_ref, hT_ref, B, T, H),
+    code = lib.tileops_gdn_prefill_fwd(*_args(q, k, v, g, beta, h0, o, hT, B, T, H),
                                        ws.data_ptr(), ws.numel(), stream)
     _native.check(code, "tileops_gdn_prefill_fwd")
+    return o, hT, need
+
+
+def _noalloc(lib, inp, B, T, H, stream):
+    q, k, v, g, beta, h0 = inp
     o = torch.full_like(v, float("nan"))
     hT = torch.full((B, H, 128, 128), float("nan"), device="cuda")
+    torch.cuda.synchronize()  # the fills (current stream) are done before `stream` runs
     code = lib.tileops_gdn_prefill_fwd_noalloc(*_args(q, k, v, g, beta, h0, o, hT, B, T, H),
                                                stream)
     _native.check(code, "tileops_gdn_prefill_fwd_noalloc")
-    torch.cuda.synchronize()
-    return o, hT, o_ref, hT_ref
+    return o, hT
 
 
 @pytest.mark.gpu
 def test_noalloc_matches_the_workspace_entry_point_on_two_calls():
-    # first call: 32 heads need 544 KiB per chunk, so the 16 MiB array holds
-    # 30 chunks and T = 2048 (32 chunks) runs as two segments
+    lib = _native.lib()
+    stream = _native.stream_of(torch.empty(1, device="cuda"))
+    # first call: 32 heads, 32 chunks -> eight segments, 13 maps per head
     B, T, H = 2, 2048, 16
-    assert (SCRATCH_BYTES // (B * H * RECORD_BYTES)) < (T + 63) // 64
-    o, hT, o_ref, hT_ref = _run_both(B, T, H, with_h0=True)
+    inp = _inputs(B, T, H, with_h0=True)
+    o_ref, hT_ref, need = _reference(lib, inp, B, T, H, stream)
+    assert need > 0  # the plan uses segment maps
+    o, hT = _noalloc(lib, inp, B, T, H, stream)
+    torch.cuda.synchronize()
     assert torch.equal(o, o_ref), "o differs (long call)"
     assert torch.equal(hT, hT_ref), "final state differs (long call)"
     # second call, smaller and ragged, from a zero state
-    o, hT, o_ref, hT_ref = _run_both(1, 300, 4, with_h0=False)
+    inp = _inputs(1, 1300, 4, with_h0=False)
+    o_ref, hT_ref, _ = _reference(lib, inp, 1, 1300, 4, stream)
+    o, hT = _noalloc(lib, inp, 1, 1300, 4, stream)
+    torch.cuda.synchronize()
     assert torch.equal(o, o_ref), "o differs (second call)"
     assert torch.equal(hT, hT_ref), "final state differs (second call)"
 
 
 @pytest.mark.gpu
-def test_noalloc_rejects_heads_beyond_the_array():
+def test_noalloc_calls_on_two_streams_do_not_race():
     lib = _native.lib()
-    H = SCRATCH_BYTES // RECORD_BYTES + 1  # one record per head no longer fits
-    fake = 256  # aligned, never dereferenced: the call returns before any launch
-    code = lib.tileops_gdn_prefill_fwd_noalloc(fake, fake, fake, fake, fake, None, fake, fake,
-                                               1, 64, H, 128, 128, 64, 0.1, BF16, None)
-    assert code == -4  # TILEOPS_EWORKSPACE
+    B, T, H = 2, 2048, 16
+    inp1 = _inputs(B, T, H, with_h0=True)
+    inp2 = _inputs(B, T, H, with_h0=False)
+    s0 = _native.stream_of(torch.empty(1, device="cuda"))
+    r1 = _reference(lib, inp1, B, T, H, s0)
+    r2 = _reference(lib, inp2, B, T, H, s0)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()  # default priority
+    o1, hT1 = _noalloc(lib, inp1, B, T, H, sa.cuda_stream)
+    o2, hT2 = _noalloc(lib, inp2, B, T, H, sb.cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, r1[0]) and torch.equal(hT1, r1[1]), "first stream's call"
+    assert torch.equal(o2, r2[0]) and torch.equal(hT2, r2[1]), "second stream's call"
+
+
+@pytest.mark.gpu
+def test_noalloc_runs_many_heads_as_one_segment():
+    # 2000 heads fill the device without splitting the sequence: no maps,
+    # no array
+    lib = _native.lib()
+    B, T, H = 1, 200, 2000
+    assert lib.tileops_gdn_prefill_workspace_bytes(B, T, H, 128, 128, 64) == 0
+    inp = _inputs(B, T, H, with_h0=False)
+    stream = _native.stream_of(inp[0])
+    o_ref, hT_ref, _ = _reference(lib, inp, B, T, H, stream)
+    o, hT = _noalloc(lib, inp, B, T, H, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref) and torch.equal(hT, hT_ref)
 
 
 @pytest.mark.gpu
 def test_noalloc_zero_length_passes_the_state_through_for_any_head_count():
-    # with T = 0 there are no chunks and no scratch is used, so the head
-    # count that the array bounds for T > 0 must not be rejected
     lib = _native.lib()
-    B, H = 1, SCRATCH_BYTES // RECORD_BYTES + 1
+    B, H = 1, 1000
     h0 = torch.randn(B, H, 128, 128, device="cuda")
     hT = torch.full_like(h0, float("nan"))
     e = torch.empty(B, 0, H, 128, device="cuda", dtype=torch.bfloat16)

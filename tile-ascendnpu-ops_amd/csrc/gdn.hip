@@ -5,31 +5,50 @@
 //   S_t = exp(g_t) S_{t-1} + beta_t k_t (v_t - exp(g_t) S_{t-1}^T k_t)^T,   o_t = scale q_t^T S_t
 //
 // Chunked (C = 64 tokens) WY form.  Inside a chunk, with gc the cumulative
-// log-decay, G[l,s] = exp(gc_l - gc_s) (l >= s), A = strictly_lower(beta_l
-// G[l,s] k_l.k_s) and T = (I + A)^-1:
-//   Tu  = T diag(beta)                                (C x C)   \ independent of S:
-//   Aqk = scale * lower_incl(G o (q k^T))             (C x C)   / kernel 1, parallel
-//   W   = Tu (v - exp(gc) o (k S))                              \
-//   o   = scale exp(gc) o (q S) + Aqk W                          > kernel 2, sequential
-//   S  <- exp(gc_C) S + k^T (exp(gc_C - gc) o W)                /  over chunks
-// (W = Tu v - w S with w = T diag(beta exp(gc)) k, regrouped so that the
-// recurrence multiplies k itself and kernel 1 hands over only two C x C
-// matrices and the per-token factors.)  Only differences gc_l - gc_s <= 0,
-// gc_C - gc_l <= 0 and gc <= 0 are ever exponentiated, so nothing overflows
-// however strong the decay.
+// log-decay, gamma = gc_C, G[l,s] = exp(gc_l - gc_s) (l >= s),
+// A = strictly_lower(beta_l G[l,s] k_l.k_s) and T = (I + A)^-1:
+//   Tu  = T diag(beta)                          \ independent of S
+//   Aqk = scale * lower_incl(G o (q k^T))        /
+//   U   = v - exp(gc) o (k S)
+//   W   = Tu U
+//   o   = scale exp(gc) o (q S) + Aqk W
+//   S  <- exp(gamma) S + k^T (exp(gamma - gc) o W)
+// Only differences gc_l - gc_s <= 0, gamma - gc_l <= 0 and gc <= 0 are ever
+// exponentiated, so nothing overflows however strong the decay.
 //
-// Kernel 1 (persistent, two workgroups per CU, the next chunk's q / k / g
-// / beta loaded while the current one is processed): K K^T and Q K^T on bf16
-// MFMA, the 64x64 unit-lower-triangular inverse in fp32 (16x16 diagonal
-// blocks by substitution, one wavefront each, the off-diagonal blocks by
-// products on fp32 MFMA), Tu, Aqk and the factors to a 17 KB record per
-// chunk.
-// Kernel 2 (one workgroup per (b, h, 32-wide slice of V), 8 wavefronts):
-// four compute wavefronts keep the state slice in MFMA accumulators
-// (wavefront i owns key rows 32i..32i+31) and exchange its bf16 copy, U =
-// v - exp(gc) o (k S) and W through LDS; four loader wavefronts bring the
-// next chunk's k, q, v slice and record into LDS with direct-to-LDS loads
-// meanwhile.  Three workgroup barriers per chunk.
+// Segments.  The chunk map S -> S' is affine, S' = A_c S + B_c, so a run of
+// chunks (a segment) maps its start state affinely too: S_end = Phi S_start
+// + Bseg, where Phi (K x K) is the segment's end state from start state I
+// with values 0, and Bseg (K x V) its end state from start state 0.  The
+// nc chunks are cut into N segments:
+//   launch 1: segment 0 runs exactly from h0 (outputs, end state), segments
+//             1 .. N-2 run from [0 | I] over 256 columns (Bseg | Phi);
+//   launch 2: segment j >= 1 composes its start state from segment 0's end
+//             state through the maps of segments 1 .. j-1, then runs
+//             exactly (outputs; the last segment writes hT).
+// The composition uses split-bf16 products (hi*hi + hi*lo + lo*hi).  With
+// N = 1 a single launch runs every chunk from h0.
+//
+// Workgroup (one per (head, segment)): NCW chain wavefronts and 4 prep
+// wavefronts (launch 1: NCW = 8, three wavefronts per SIMD; launch 2 and
+// single-segment runs: NCW = 4, two per SIMD):
+//   chain      hold the state in MFMA accumulators, all 128 key rows of
+//              their columns (16 or 32 value columns in an exact segment,
+//              32 of Bseg or Phi in a map segment), so that the
+//              chunk step P = k S -> U -> W = Tu U -> S' runs in registers:
+//              an accumulator is fed to the next product as it stands, the
+//              rows of each product being chosen so that its accumulator
+//              rows land in the order the next product's k-slots expect;
+//              in exact segments they also form o and their share of Aqk;
+//   prep       prepare the chunks ahead while the chain runs the current
+//              one: k k^T products and diagonal blocks of T (blocked
+//              substitution, products on fp32 MFMA) for the next chunk, the
+//              rest of T and Tu (into LDS) for the current one, the decay
+//              scan two chunks ahead, and the direct-to-LDS loads of the
+//              chunk operands (the chain wavefronts form Aqk, and L21 when
+//              there are four of them).
+// Three workgroup barriers per chunk.  Every chunk operand crosses HBM once
+// per pass over its segment, and nothing per chunk is written back.
 #include <algorithm>
 #include <mutex>
 
@@ -46,37 +65,66 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int C = 64;    // chunk length
 constexpr int DK = 128;  // key dim
 constexpr int DV = 128;  // value dim
-constexpr int VS = 32;   // value columns per kernel-2 workgroup
-constexpr int KP = DK + 8;  // LDS row stride of a natural [C][DK] tile (elements)
-constexpr int CP = C + 8;   // LDS row stride of a transposed [*][C] tile (elements)
+constexpr int kMaxSeg = 16;
+constexpr int DS = 36;  // fp32 row stride of the diagonal 32x32 blocks of A^T / T
+constexpr int XS = 36;  // fp32 row stride of X
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr size_t kStateFloats = (size_t)DK * DV;
 
-// workspace record per chunk
-constexpr size_t kTuOff = 0;                                  // Tu   [C][C] bf16
-constexpr size_t kAqkOff = kTuOff + (size_t)C * C * 2;        // Aqk  [C][C] bf16
-constexpr size_t kFacOff = kAqkOff + (size_t)C * C * 2;       // factors, f32 [kFacN]
-constexpr int kFacN = 256;
-// factor slots: scale e^{gc_l}, e^{gc_l}, e^{gc_C - gc_l} (l < C), e^{gc_C}
-constexpr int kFacOut = 0, kFacG = C, kFacD = 2 * C, kFacChunk = 3 * C;
-constexpr size_t kChunkBytes = kFacOff + (size_t)kFacN * 4;  // 17,408
+// per-chunk factors (fp32, LDS): scale e^{gc}, e^{gc}, e^{gamma - gc}, gc,
+// beta (rows past T zero), e^{gamma}
+constexpr int kFacSE = 0, kFacE = 64, kFacD = 128, kFacGC = 192, kFacB = 256, kFacEG = 320;
+constexpr int kFacN = 336;
 
-__device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+struct Args {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  const float* g;
+  const float* beta;
+  const float* h0;
+  bf16* o;
+  float* hT;
+  float* ws;  // per head: segment 0's end state, then (Phi_j, Bseg_j), j = 1 .. N-2
+  int B, T, H;
+  float scale;
+  int nseg;
+  int phase;               // 1 or 2
+  int start[kMaxSeg + 1];  // first chunk of each segment; start[nseg] = chunk count
+};
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
-
-__device__ __forceinline__ bf16x8 ld8(const bf16* p) {  // 16-byte load (LDS or global)
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
-
+__device__ __forceinline__ bf16x8 pack8(f32x4 a, f32x4 b) {
+  bf16x8 r;
+  r[0] = (bf16)a[0];
+  r[1] = (bf16)a[1];
+  r[2] = (bf16)a[2];
+  r[3] = (bf16)a[3];
+  r[4] = (bf16)b[0];
+  r[5] = (bf16)b[1];
+  r[6] = (bf16)b[2];
+  r[7] = (bf16)b[3];
+  return r;
+}
+// Four fp32 values as four bf16 in one 8-byte word.
+__device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d) {
+  bf16 p[4] = {(bf16)a, (bf16)b, (bf16)c, (bf16)d};
+  return *reinterpret_cast<uint2*>(p);
+}
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Inclusive prefix sum over the 64 lanes of a wavefront by DPP lane moves,
-// with no LDS round trip (a shuffle-based scan waits on the LDS queue, which
-// the other workgroups of the CU keep busy): Hillis-Steele inside each row
-// of 16 lanes (row_shr 1, 2, 4, 8; lanes shifted in from outside the row
-// read 0), then each row's total carried forward: row_bcast:15 adds lane
-// 16 r + 15 to row r + 1 (rows 1 and 3), row_bcast:31 adds lane 31 to rows
-// 2 and 3.
+// Inclusive prefix sum over the 64 lanes of a wavefront by DPP lane moves:
+// Hillis-Steele inside each row of 16 lanes (row_shr 1, 2, 4, 8; lanes
+// shifted in from outside the row read 0), then each row's total carried
+// forward (row_bcast:15 to rows 1 and 3, row_bcast:31 to rows 2 and 3).
 __device__ __forceinline__ float dpp_add(float x, int moved) {
   return x + __builtin_bit_cast(float, moved);
 }
@@ -95,10 +143,10 @@ __device__ __forceinline__ float wave_inclusive_sum(float x) {
 
 // Workgroup barrier that waits only for this wavefront's LDS accesses
 // (lgkmcnt(0); vmcnt and expcnt left at their maxima), so that global loads
-// and stores issued before it stay in flight across it (direct-to-LDS loads
-// included).  __syncthreads() would also wait for them: its fence drains
-// every outstanding memory access.  Only LDS data is exchanged through these
-// barriers; register results of global loads are waited for at their use.
+// and stores issued before it stay in flight across it.  Only LDS data is
+// exchanged through these barriers; the direct-to-LDS loads are waited for
+// explicitly (vmcnt) by the wavefronts that issued them, before the barrier
+// that publishes them.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xC07F);
   asm volatile("" ::: "memory");
@@ -106,313 +154,59 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Four fp32 values as four bf16 in one 8-byte word.
-__device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d) {
-  bf16 p[4] = {(bf16)a, (bf16)b, (bf16)c, (bf16)d};
-  return *reinterpret_cast<uint2*>(p);
+// LDS values written by other lanes of the same wavefront are read back
+// after these fences: the LDS operations of one wavefront execute in order,
+// and the fences keep the compiler from moving the reads above the writes.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // ---------------------------------------------------------------------------
-// kernel 1: per-chunk preparation
+// LDS images.  Rows of 128 (k, q, v) or 64 (Tu, Aqk) bf16 are stored
+// unpadded with their 16-byte chunks XOR-swizzled by row, so that the three
+// read patterns touch distinct bank groups: 16 consecutive rows at one chunk
+// (natural operand rows), the 16 rows 8 (m / 4) + 4 b + m % 4 of a block
+// (the rows a chain product reads, lam()), and transpose reads (4
+// consecutive rows x 4 8-byte words).
 // ---------------------------------------------------------------------------
-// LDS plan (three workgroups would fit one CU; two run per CU, so that the
-// kernel keeps every value in registers: at three the compiler spills):
-//   r0: k natural [C][KP] bf16 (K K^T)            -> T (fp32 [C][AS], inverse)
-//   r1: A^T fp32 [C][AS] (A^T[m][i] = A[i][m])
-//   x_s: A10 T00 / A32 T22 / A21 T11 (fp32)
-constexpr int AS = 72;  // fp32 row stride of A^T / T (288 bytes: float4-aligned rows)
-constexpr int XS = 36;  // fp32 row stride of X
+__device__ __forceinline__ int sw16(int r) {
+  return (r & 15) ^ ((r & 3) << 2) ^ (((r >> 4) & 1) << 2);
+}
+__device__ __forceinline__ int off128(int r, int p) { return r * 128 + ((p ^ sw16(r)) << 3); }
+__device__ __forceinline__ int sw8(int r) {
+  return ((r >> 1) & 1) | (((r >> 3) & 1) << 1) | ((((r >> 2) ^ (r >> 4)) & 1) << 2);
+}
+__device__ __forceinline__ int off64(int r, int p) { return r * 64 + ((p ^ sw8(r)) << 3); }
+// [32][32] images (4 chunks per row): chunk p ^ ((r / 8) % 4)
+__device__ __forceinline__ int off32(int r, int p) { return r * 32 + ((p ^ ((r >> 3) & 3)) << 3); }
 
-// Global operands of one chunk for one thread, loaded a chunk ahead: 16
-// bytes (dims 8 (tid & 15) ..) of k and q rows 16 i + tid / 16 (i < 4), so
-// that every load instruction reads four whole 256-byte rows, and g / beta
-// of token `lane`.  Rows past T load the chunk's last row and are zeroed
-// where they are staged.
-struct PrepLoads {
-  u32x4 kr[4], qr[4];
-  float g, beta;
-};
-
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_prep_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ g,
-    const float* __restrict__ beta, uint8_t* __restrict__ ws, int B, int T, int H, int c0, int NS,
-    float scale) {
-  __shared__ __attribute__((aligned(16))) float r0[C * AS];
-  __shared__ __attribute__((aligned(16))) float r1[C * AS];
-  __shared__ __attribute__((aligned(16))) float x_s[32 * XS];
-  __shared__ __attribute__((aligned(16))) float gc_s[C], beta_s[C];
-  __shared__ __attribute__((aligned(16))) bf16 q_s[C * KP];
-  static_assert(C * KP * 2 <= C * AS * 4, "k tile must fit the T region");
-  bf16* k_s = reinterpret_cast<bf16*>(r0);
-  float* t_s = r0;
-  float* at_s = r1;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 31, half = lane >> 5;
-  const int rb = wave == 0 ? 0 : 1;  // Q K^T / K K^T block of waves 0-2
-  const int cb = wave == 2 ? 1 : 0;
-  const int lrow = tid >> 4, lchk = tid & 15;  // row (of 16) and 16-byte chunk of the loads
-  const int64_t tok_stride = (int64_t)H * DK;  // DK == DV
-  // record blk of the workspace: (b, h) = blk / NS, chunk c0 + blk % NS
-  const uint64_t nblk = (uint64_t)B * H * NS;
-
-  auto load = [&](uint64_t blk, PrepLoads& L) {
-    const int chunk = c0 + (int)(blk % NS), bh = (int)(blk / NS);
-    const int h = bh % H, b = bh / H;
-    const int t0 = chunk * C, n = min(C, T - t0);
-    const int64_t off0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK + lchk * 8;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t off = off0 + (int64_t)min(16 * i + lrow, n - 1) * tok_stride;
-      L.kr[i] = *reinterpret_cast<const u32x4*>(k + off);
-      L.qr[i] = *reinterpret_cast<const u32x4*>(q + off);
-    }
-    const int64_t gi = ((int64_t)b * T + t0 + min(lane, n - 1)) * H + h;
-    L.g = g[gi];
-    L.beta = beta[gi];
-  };
-
-  // Persistent: workgroup i takes chunks i, i + grid, ...; the next chunk's
-  // loads are issued as soon as the current one's registers are consumed.
-  PrepLoads cur;
-  // (see the settle before the record stores below; here for the first
-  // chunk's loads, so that both paths into the loop arrive settled)
-  auto settle = [&]() {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(cur.kr[i]), "+v"(cur.qr[i]));
-    asm volatile("" : "+v"(cur.g), "+v"(cur.beta));
-  };
-  uint64_t blk = blockIdx.x;
-  if (blk < nblk) load(blk, cur);
-  settle();
-  for (; blk < nblk; blk += gridDim.x) {
-    const int chunk = c0 + (int)(blk % NS);
-    const int t0 = chunk * C;
-    const int n = min(C, T - t0);
-    uint8_t* wsc = ws + (size_t)blk * kChunkBytes;
-    bf16* tu_ws = reinterpret_cast<bf16*>(wsc + kTuOff);
-    bf16* aqk_ws = reinterpret_cast<bf16*>(wsc + kAqkOff);
-    float* fac_ws = reinterpret_cast<float*>(wsc + kFacOff);
-
-    // ---- stage k and q; rows past T are 0
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 16 * i + lrow;
-      if (row >= n) cur.kr[i] = cur.qr[i] = u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(k_s + row * KP + lchk * 8) = cur.kr[i];
-      *reinterpret_cast<u32x4*>(q_s + row * KP + lchk * 8) = cur.qr[i];
-    }
-    if (wave == 3) {
-      float x = lane < n ? cur.g : 0.0f;
-      const float bt = lane < n ? cur.beta : 0.0f;
-      x = wave_inclusive_sum(x);  // gc: inclusive prefix sum over the chunk
-      gc_s[lane] = x;
-      beta_s[lane] = bt;
-      // the factors the recurrence applies: scale e^{gc} per output row,
-      // e^{gc} on k S, e^{gc_C - gc} on W for the state update, e^{gc_C}
-      const float gl = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), C - 1));
-      const float eg = exp2f_fast(x * kLog2e);
-      fac_ws[kFacOut + lane] = scale * eg;
-      fac_ws[kFacG + lane] = eg;
-      fac_ws[kFacD + lane] = exp2f_fast((gl - x) * kLog2e);
-      fac_ws[kFacChunk + lane] = lane == 0 ? exp2f_fast(gl * kLog2e) : 0.0f;
-    }
-    lds_barrier();
-
-    // ---- K K^T -> A^T (fp32, LDS) and Q K^T -> Aqk (bf16, to the record),
-    // in 32x32 blocks (row block rb, column block cb).  Only the strictly
-    // lower parts of the diagonal blocks and the block A21 of A are ever
-    // read back; the block l < 32 <= s of Aqk is zero.
-    if (wave < 3) {
-      // transposed orientation: k rows s of block cb as the A operand, k / q
-      // rows l of block rb as B, so that a lane owns one row l (column of the
-      // result) and its 16 values run over s: [s][l] = k_s . k_l and k_s . q_l
-      f32x16 kk = {}, qk = {};
-#pragma unroll
-      for (int ks = 0; ks < DK / 16; ++ks) {
-        const bf16x8 bs = ld8(k_s + (cb * 32 + col) * KP + ks * 16 + half * 8);
-        const bf16x8 bl = ld8(k_s + (rb * 32 + col) * KP + ks * 16 + half * 8);
-        const bf16x8 a = ld8(q_s + (rb * 32 + col) * KP + ks * 16 + half * 8);
-        kk = mfma(bs, bl, kk);
-        qk = mfma(bs, a, qk);
-      }
-      const int l = rb * 32 + col;
-      const float gl = gc_s[l], bel = beta_s[l];
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int s0 = cb * 32 + g4 * 8 + half * 4;
-        const float4 gs4 = *reinterpret_cast<const float4*>(gc_s + s0);
-        const float gsv[4] = {gs4.x, gs4.y, gs4.z, gs4.w};
-        float qv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = g4 * 4 + e;
-          const int sc = s0 + e;
-          // branch-free: the decay is evaluated for every element (its
-          // argument clamped to <= 0, exact where it is used) and selected
-          float gd = exp2f_fast(fminf((gl - gsv[e]) * kLog2e, 0.0f));
-          asm volatile("" : "+v"(gd));
-          gd = sc <= l ? gd : 0.0f;
-          at_s[sc * AS + l] = sc < l ? bel * gd * kk[r] : 0.0f;  // A^T[s][l]
-          qv[e] = scale * gd * qk[r];
-        }
-        *reinterpret_cast<uint2*>(aqk_ws + l * C + s0) = pack_bf16x4(qv[0], qv[1], qv[2], qv[3]);
-      }
-    } else {
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4)
-        *reinterpret_cast<uint2*>(aqk_ws + col * C + 32 + g4 * 8 + half * 4) = make_uint2(0u, 0u);
-    }
-    if (blk + gridDim.x < nblk) load(blk + gridDim.x, cur);  // operands consumed: next chunk
-    lds_barrier();
-
-    // ---- T = (I + A)^-1, blocked by 16: the four diagonal blocks Tbb by
-    // substitution (wave w: block w, lane j: column j; p[i] accumulates
-    // sum_m A[i][m] T[m][j]), then on fp32 MFMA T10 = -T11 (A10 T00),
-    // T32 = -T33 (A32 T22) and, with 32-row blocks, T21 = -T22 (A21 T11).
-    {
-      const int base = 16 * wave, jl = lane & 15;
-      float p[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) p[i] = 0.0f;
-      // av[m & 1][gq] = A[base + 4gq .. 4gq + 3][base + m]; step m + 1's
-      // groups are read while step m's FMAs run
-      const float4* a4p = reinterpret_cast<const float4*>(at_s + base * AS + base);
-      float4 av[2][4];
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) av[0][gq] = a4p[gq];
-#pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        if (m + 1 < 16) {
-#pragma unroll
-          for (int gq = (m + 2) >> 2; gq < 4; ++gq) av[(m + 1) & 1][gq] = a4p[(m + 1) * (AS / 4) + gq];
-        }
-        const float t = (m == jl ? 1.0f : 0.0f) - p[m];
-        // every lane writes (the four 16-lane groups hold the same columns,
-        // so the writes agree): no exec-masked branch in the chain
-        t_s[(base + m) * AS + base + jl] = t;
-#pragma unroll
-        for (int gq = (m + 1) >> 2; gq < 4; ++gq) {
-          const float4 a4 = av[m & 1][gq];
-          const int i4 = 4 * gq;
-          if (i4 + 0 > m) p[i4 + 0] = fmaf(a4.x, t, p[i4 + 0]);
-          if (i4 + 1 > m) p[i4 + 1] = fmaf(a4.y, t, p[i4 + 1]);
-          if (i4 + 2 > m) p[i4 + 2] = fmaf(a4.z, t, p[i4 + 2]);
-          if (i4 + 3 > m) p[i4 + 3] = fmaf(a4.w, t, p[i4 + 3]);
-        }
-      }
-    }
-    lds_barrier();
-    // v_mfma_f32_16x16x4f32 lanes: A[mi][mk], B[mk][mi], D[4 mk + r][mi]
-    const int mi = lane & 15, mk = lane >> 4;
-    if (wave < 2) {  // Y = A10 T00 (wave 0) / A32 T22 (wave 1) -> x_s rows 16 wave ..
-      const int d0 = 32 * wave;
-      f32x4 y = {};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int kx = 4 * kk + mk;
-        y = __builtin_amdgcn_mfma_f32_16x16x4f32(at_s[(d0 + kx) * AS + d0 + 16 + mi],
-                                                t_s[(d0 + kx) * AS + d0 + mi], y, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x_s[(16 * wave + 4 * mk + r) * XS + mi] = y[r];
-    }
-    // no barrier: each of waves 0, 1 reads back only its own Y rows, T11 /
-    // T33 are settled since the substitution's barrier, and the zero blocks
-    // written below are read by no wavefront before the next barrier.  Lanes
-    // read Y values other lanes of the same wavefront wrote: the fences keep
-    // the compiler from moving those LDS reads above the writes (the LDS
-    // operations of one wavefront execute in order, so no s_barrier is needed)
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (wave < 2) {  // T10 = -T11 Y (wave 0), T32 = -T33 Y (wave 1)
-      const int d0 = 32 * wave;
-      f32x4 z = {};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int kx = 4 * kk + mk;
-        z = __builtin_amdgcn_mfma_f32_16x16x4f32(t_s[(d0 + 16 + mi) * AS + d0 + 16 + kx],
-                                                x_s[(16 * wave + kx) * XS + mi], z, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) t_s[(d0 + 16 + 4 * mk + r) * AS + d0 + mi] = -z[r];
-    } else {  // the upper blocks T01, T23 are zero
-      const int d0 = 32 * (wave - 2);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) t_s[(d0 + 4 * mk + r) * AS + d0 + 16 + mi] = 0.0f;
-    }
-    lds_barrier();
-    const int qi = wave >> 1, qj = wave & 1;  // 16x16 quadrant of a 32x32 block
-    {  // X = A21 T11 -> x_s
-      f32x4 x = {};
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const int kx = 4 * kk + mk;
-        x = __builtin_amdgcn_mfma_f32_16x16x4f32(at_s[kx * AS + 32 + 16 * qi + mi],
-                                                t_s[kx * AS + 16 * qj + mi], x, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x_s[(16 * qi + 4 * mk + r) * XS + 16 * qj + mi] = x[r];
-    }
-    lds_barrier();
-    {  // T21 = -T22 X
-      f32x4 y = {};
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const int kx = 4 * kk + mk;
-        y = __builtin_amdgcn_mfma_f32_16x16x4f32(t_s[(32 + 16 * qi + mi) * AS + 32 + kx],
-                                                x_s[kx * XS + 16 * qj + mi], y, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) t_s[(32 + 16 * qi + 4 * mk + r) * AS + 16 * qj + mi] = -y[r];
-    }
-    lds_barrier();
-
-    // The next chunk's operands (loaded after the products above) pass
-    // through an empty asm before the record stores below: the compiler
-    // resolves their loads here, while only older stores are in flight.
-    // Otherwise its bookkeeping across the loop places those waits at their
-    // first use, after these stores, and waits for the stores as well.
-    settle();
-
-    // ---- Tu = T diag(beta) in bf16 to the record (T12 is zero); 4
-    // consecutive columns per thread: float4 in, one 8-byte store out
-#pragma unroll
-    for (int e = tid; e < C * C / 4; e += 256) {
-      const int i = e >> 4, j = (e & 15) * 4;
-      const float4 t = (i < 32 && j >= 32) ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                                           : *reinterpret_cast<const float4*>(t_s + i * AS + j);
-      const float4 bt = *reinterpret_cast<const float4*>(beta_s + j);
-      *reinterpret_cast<uint2*>(tu_ws + i * C + j) =
-          pack_bf16x4(t.x * bt.x, t.y * bt.y, t.z * bt.z, t.w * bt.w);
-    }
-    lds_barrier();  // LDS is rewritten by the next chunk
-  }
+// Row read by lane-row m of the A operand for output block blk (16 rows of
+// the 32-row group blk / 2).  Then accumulator row 4 g + r of block blk
+// (lane group g) holds logical row acc_row(blk, g, r) = 32 (blk / 2) + 8 g +
+// 4 (blk % 2) + r, so that blocks 2j and 2j + 1 of an accumulator, taken as
+// the 8 k-slots 8 g + e of a 16x16x32 operand (e < 4 from block 2j, e >= 4
+// from block 2j + 1), hold rows 32 j + 8 g + e: natural order.
+// A lane index the compiler cannot see through: addresses derived from it are
+// recomputed where they are used instead of being held in registers across
+// the chunk loop (dozens of per-lane swizzled LDS addresses otherwise stay
+// live and push the state out to scratch).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
 }
 
-// ---------------------------------------------------------------------------
-// kernel 2: the sequential recurrence over chunks and the output
-// ---------------------------------------------------------------------------
-// LDS images of one chunk's operands.  They are filled straight from memory
-// by direct-to-LDS loads (global_load_lds_dwordx4: the 16 bytes of lane l
-// land at base + 16 l, every lane choosing its own source address), one
-// chunk ahead, into two slots.  Rows are stored unpadded with their 16-byte
-// chunks XOR-swizzled by row, so that an MFMA operand read (16 consecutive
-// rows, one chunk each) touches 16 distinct bank groups.
-struct ChunkSlot {
-  bf16 k[C * DK];    // k rows l: chunk p of row l holds chunk p ^ (l & 15)
-  bf16 q[C * DK];    // q rows, same swizzle
-  bf16 tu[C * C];    // Tu rows: chunk p holds chunk p ^ ((l >> 1) & 7)
-  bf16 aqk[C * C];   // Aqk rows, same
-  bf16 v[C * VS];    // v slice rows [token][VS], unswizzled (read transposed)
-  float fac[kFacN];  // the record's factors
-};
+// Keeps the scheduler from moving instructions across this point: operand
+// reads issued before it stay ahead of the products after it, so that the
+// LDS latency of one step overlaps the MFMAs of the previous one.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// element offset of 16-byte chunk `kc` of row `r` in a swizzled image with
-// 128-element (16-chunk) or 64-element (8-chunk) rows
-__device__ __forceinline__ int swz16(int r, int kc) { return r * DK + ((kc ^ (r & 15)) << 3); }
-__device__ __forceinline__ int swz8(int r, int kc) { return r * C + ((kc ^ ((r >> 1) & 7)) << 3); }
+__device__ __forceinline__ int lam(int blk, int m) {
+  return 32 * (blk >> 1) + 8 * (m >> 2) + 4 * (blk & 1) + (m & 3);
+}
+__device__ __forceinline__ int acc_row(int blk, int g, int r) {
+  return 32 * (blk >> 1) + 8 * g + 4 * (blk & 1) + r;
+}
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
@@ -420,356 +214,805 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_void_ptr)p;
 }
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives element
+// i % 4 of the 8 bytes addressed by lanes i / 4, 4 + i / 4, 8 + i / 4 and
+// 12 + i / 4 (in that order).
+__device__ __forceinline__ v4i16 ds_read_tr(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)lds_addr(p));
+}
 
-// Direct-to-LDS loads: lane l reads 16 (4) bytes at `base + off` (base
-// uniform, in SGPRs; off a per-lane byte offset) and they land at LDS byte
-// address lds + 16 l (4 l).  Issued as inline assembly so that the compiler
-// does not track the LDS writes: otherwise it waits for every outstanding
-// vector memory operation (the output stores included) before each LDS
-// access of the compute wavefronts.  Every wait for these loads is explicit
-// (vmcnt) and followed by a workgroup barrier before any wavefront reads
-// the data.
+// Direct-to-LDS loads: lane l reads 16 bytes at `base + off` (base uniform,
+// in SGPRs) landing at LDS address lds + 16 l, or 4 bytes at a per-lane
+// address landing at lds + 4 l.  Inline assembly, so that the compiler does
+// not track the LDS writes; every wait for them is explicit.
 // A wavefront-uniform pointer moved into SGPRs: both 32-bit halves are read
-// from the first active lane and joined as unsigned words (readfirstlane
-// returns int, which must not be sign-extended into the high word).
+// from the first active lane and joined as unsigned words.
 __device__ __forceinline__ const void* uniform_ptr(const void* p) {
   const uint64_t a = reinterpret_cast<uint64_t>(p);
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
   return reinterpret_cast<const void*>(((uint64_t)hi << 32) | (uint64_t)lo);
 }
-
 // The compiler's hazard checks do not look into inline assembly, so each
 // load starts with the wait states the ISA requires before it: 5 after a
-// VALU write (v_readfirstlane) of an SGPR the load reads (its base), 1
-// after the SALU write of M0.
+// VALU write (v_readfirstlane) of an SGPR the load reads, 1 after the SALU
+// write of M0.
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(uniform_ptr(base)),
                "{m0}"(lds) : "memory");
 }
+__device__ __forceinline__ void lds_dma4(const void* addr, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, off" : : "v"(addr), "{m0}"(lds) : "memory");
+}
 
-// Fill the swizzled image `dst` (NCH 16-byte chunks, CPR per row) from the
-// rows `src + min(r, rmax) * stride` (elements; `src` uniform).  Each of the
-// 4 wavefronts issues every 4th 1 KB window (64 chunks).
-template <int CPR, int NCH>
-__device__ __forceinline__ void gather_rows(bf16* dst, const bf16* src, int64_t stride, int rmax,
-                                            int wave, int lane) {
-  static_assert(NCH % 256 == 0, "whole windows for every wavefront");
+// Fill a swizzled [64][128] bf16 image from rows `src + min(r, rmax) *
+// stride` (elements, src uniform): 16 windows of 1 KB, loader lw (0, 1)
+// issuing every second one.
+__device__ __forceinline__ void fill128(bf16* img, const bf16* src, int64_t stride, int rmax,
+                                        int lw, int lane) {
 #pragma unroll
-  for (int i = 0; i < NCH / 256; ++i) {
-    const int win = 4 * i + wave;
+  for (int i = 0; i < 8; ++i) {
+    const int win = 2 * i + lw;
     const int ch = win * 64 + lane;
-    const int r = ch / CPR, p = ch % CPR;
-    const int key = CPR == 16 ? (r & 15) : CPR == 8 ? ((r >> 1) & 7) : 0;
-    const uint32_t off = (uint32_t)(((int64_t)min(r, rmax) * stride + ((p ^ key) << 3)) * 2);
-    lds_dma16(src, off, lds_addr(dst + win * 512));
+    const int r = ch >> 4;
+    const int p = (ch & 15) ^ sw16(r);
+    const uint32_t off = (uint32_t)(((int64_t)min(r, rmax) * stride + (p << 3)) * 2);
+    lds_dma16(src, off, lds_addr(img + win * 512));
   }
 }
 
-// The kernel runs chunks c0 .. c1 - 1 of every head, reading their records
-// at (b H + h) NS + (c - c0) of the workspace, starting from state h0 (zero
-// when null) and leaving the state in hT.  h0 may be hT itself (a segment
-// continuing the previous one): each workgroup reads its own state slice
-// before its first chunk and writes it after its last.
-__global__ __launch_bounds__(512) void gdn_recur_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const float* h0, const uint8_t* __restrict__ ws, bf16* __restrict__ o, float* hT, int B,
-    int T, int H, int c0, int c1, int NS) {
-  constexpr int SP = DK + 8;  // row stride of S^T [v][d]
-  // two separate objects, so that the compiler can tell a slot being read
-  // from the one the direct-to-LDS loads are filling
-  __shared__ __attribute__((aligned(16))) ChunkSlot slot0;
-  __shared__ __attribute__((aligned(16))) ChunkSlot slot1;
-  __shared__ __attribute__((aligned(16))) bf16 st_s[VS * SP];      // bf16 S^T (slice)
-  __shared__ __attribute__((aligned(16))) bf16 ut_s[VS * CP];      // U^T (slice)
-  __shared__ __attribute__((aligned(16))) bf16 wt_s[VS * CP];      // W^T (slice)
-  __shared__ __attribute__((aligned(16))) bf16 dwt_s[VS * CP];     // (e^{gc_C - gc} o W)^T
-  __shared__ __attribute__((aligned(16))) uint32_t touch_s[64];    // landing area of L2 prefetches
+struct Smem {
+  bf16 k[3][C * DK];     // k of chunks c, c + 1, c + 2 (slot c % 3)
+  bf16 q[2][C * DK];     // q of chunks c, c + 1 (slot c % 2)
+  bf16 v[C * DV];        // v of chunk c (then c + 1, loaded once U is formed)
+  bf16 tu[2][32 * 32];   // Tu11 | Tu22 of chunk c (then c + 1)
+  bf16 l21[2][32 * 32];  // L21 of chunks c, c + 1 (slot c % 2)
+  bf16 aqk[C * C];       // Aqk of chunk c
+  float fac[3][kFacN];   // factors of chunks c .. c + 2 (slot c % 3)
+  float gb[4][2 * C];    // raw g | beta of chunks c .. c + 3 (slot c % 4)
+  float at[2][C * DS];   // A^T of chunks c, c + 1 (slot c % 2): the diagonal 32x32 blocks
+  float t[C * DS];       // T of chunk c + 1 (then c + 2), the diagonal 32x32 blocks
+  float x[32 * XS];      // products of the block inverse
+};
+static_assert(sizeof(Smem) <= 163840, "the LDS of one CU");
 
-  // waves 0-3 compute; waves 4-7 (one per SIMD beside them) only move the
-  // next chunk's operands, so that the bounded rate of the CU's load path
-  // never holds up a compute wavefront's instruction stream
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool loader = wave >= 4;
-  const int lw = wave & 3;     // index among the loaders / among the compute waves
-  const int ltid = tid & 255;  // thread index inside its group of four wavefronts
+// ---------------------------------------------------------------------------
+// The preparation of one chunk (prep wavefronts pw = 0 .. 3)
+// ---------------------------------------------------------------------------
+// The inverse in halves.  With T = (I + A)^-1 = [[T11, 0], [T21, T22]]
+// (32-row blocks) and A21 = diag(beta_bot) L21, L21[l - 32][s] = G[l][s]
+// k_l.k_s, T21 = -T22 A21 T11, so W = T diag(beta) U is
+//   W_top = Tu11 U_top,   W_bot = Tu22 (U_bot - L21 W_top),   Tuii = Tii diag(beta_i):
+// the preparation forms only the diagonal blocks Tu11, Tu22 and L21; the
+// chain applies the coupling.  A^T and T keep only the two diagonal 32x32
+// blocks: element (r, c), with r and c in the same block, at r * DS + c % 32.
+//
+// PA: the 32x32 block blk of G o (k k^T), blk 0: (l, s) in 00, 1: in 11,
+// 2: l in 32-63, s in 0-31 (L21), in the transposed orientation (k rows s
+// as the A operand, so that a lane owns one row l and its 16 values run
+// over s); blocks 00 and 11 become A^T[s][l] = beta_l G[l][s] k_l.k_s
+// (s < l, fp32), block 10 is stored as L21 (bf16).  The operands of BATCH
+// key steps are read at a time (8: all in flight; fewer where registers
+// are scarce).
+template <int BATCH>
+__device__ __forceinline__ void prep_products(const bf16* kimg, const float* fc, float* at,
+                                              bf16* l21, int blk, int lane) {
   const int col = lane & 31, half = lane >> 5;
-  // the VS-slices of one head run on the same XCD (they share q, k and the
-  // chunk records through its L2)
-  const int total = gridDim.x;
-  int id = blockIdx.x;
-  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
-  const int nvs = DV / VS;
-  const int vs = id % nvs;
-  const int bh = id / nvs;
-  const int h = bh % H, b = bh / H;
-  const int v0 = vs * VS;
-  const int64_t tok_stride = (int64_t)H * DK;
-  const int rblk = wave & 1;         // chunk rows 32*rblk .. 32*rblk+31 (A operands)
-  const int arow = rblk * 32 + col;  // A-operand row of this lane
-
-  // k^T (A operand of the state update) through transpose reads of the
-  // natural k image: in each group of 16 lanes, lane j points at 4 dims
-  // (d0 + 4 (j % 4) ..) of token row t0 + j / 4 and receives dim d0 + j of
-  // those 4 tokens.  Lane group g covers dims 32 wave + 16 (g & 1) .. and
-  // tokens 8 (g >> 1) .. of each 16-token step; the second read takes the
-  // next 4 tokens.  The swizzle key (t & 15) does not depend on the step, so
-  // the step is a constant 16-row (4 KB) offset.
-  int ktoff[2] = {0, 0};
-  if (!loader) {
-    const int g16 = lane >> 4, j16 = lane & 15;
-    const int dd = 32 * wave + 16 * (g16 & 1) + 4 * (j16 & 3);
+  const int rb = blk == 0 ? 0 : 1, cb = blk == 1 ? 1 : 0;
+  f32x16 kk = {};
 #pragma unroll
-    for (int rd = 0; rd < 2; ++rd) {
-      const int t = 8 * (g16 >> 1) + 4 * rd + (j16 >> 2);
-      ktoff[rd] = t * DK + (((dd >> 3) ^ (t & 15)) << 3) + (dd & 7);
+  for (int k0 = 0; k0 < DK / 16; k0 += BATCH) {
+    bf16x8 bs[BATCH], bl[BATCH];
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      bs[i] = ld8(kimg + off128(cb * 32 + col, 2 * (k0 + i) + half));
+      bl[i] = ld8(kimg + off128(rb * 32 + col, 2 * (k0 + i) + half));
     }
+    sched_fence();
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) kk = mfma32(bs[i], bl[i], kk);
   }
-  // v^T (columns of the natural v image) for the U update: 4 consecutive
-  // token rows (32 rblk + 8 g4 + 4 half ..) of v column `col`, by the same
-  // transpose read: lane j of a 16-lane group points at 4 columns
-  // (16 (g & 1) + 4 (j % 4) ..) of token row 4 (g >> 1) + j / 4 (+ the g4
-  // and rblk terms, constants of 8 and 32 rows).
-  int vtoff = 0;
-  {
-    const int g16 = lane >> 4, j16 = lane & 15;
-    vtoff = (32 * rblk + 4 * (g16 >> 1) + (j16 >> 2)) * VS + 16 * (g16 & 1) + 4 * (j16 & 3);
-  }
-  auto read_vt4 = [&](const bf16* vimg, int g4) -> uint2 {
-    const uint32_t a = lds_addr(vimg) + (uint32_t)((vtoff + g4 * 8 * VS) * 2);
-    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)a));
-  };
-  auto read_kt = [&](const bf16* kimg, int ks) -> bf16x8 {
-    const uint32_t base = lds_addr(kimg) + (uint32_t)(ks * 16 * DK * 2);
-    const v4i16 x0 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(base + ktoff[0] * 2));
-    const v4i16 x1 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(base + ktoff[1] * 2));
-    const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
-    const u32x4 w4 = {y0.x, y0.y, y1.x, y1.y};
-    return __builtin_bit_cast(bf16x8, w4);
-  };
-
-  // chunk c's operands (loader wavefronts), all by direct-to-LDS loads into
-  // the images of slot `sl`, in two parts so that the CU's load path is busy
-  // in two phases of a step rather than one: the q and k rows, then the
-  // record and the v slice.
-  // Rows past T are clamped onto the chunk's last row rather than zeroed:
-  // their k only meets columns of Tu and rows of W that are exactly zero
-  // (beta = 0 there), their v only those columns of Tu, and their q only
-  // output rows that are not stored.
-  auto load_rows = [&](int c, ChunkSlot& sl) {
-    const int t0 = c * C;
-    const int last = min(C, T - t0) - 1;
-    const int64_t row0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK;
-    gather_rows<16, C * DK / 8>(sl.k, k + row0, tok_stride, last, lw, lane);
-    gather_rows<16, C * DK / 8>(sl.q, q + row0, tok_stride, last, lw, lane);
-  };
-  auto load_record = [&](int c, ChunkSlot& sl) {
-    const int t0 = c * C;
-    const int last = min(C, T - t0) - 1;
-    const uint8_t* wsc = ws + (((size_t)b * H + h) * NS + (c - c0)) * kChunkBytes;
-    const int64_t row0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DV;
-    gather_rows<8, C * C / 8>(sl.tu, reinterpret_cast<const bf16*>(wsc + kTuOff), C, C - 1, lw,
-                              lane);
-    gather_rows<8, C * C / 8>(sl.aqk, reinterpret_cast<const bf16*>(wsc + kAqkOff), C, C - 1,
-                              lw, lane);
-    gather_rows<VS / 8, C * VS / 8>(sl.v, v + row0 + v0, tok_stride, last, lw, lane);
-    if (lw == 0) lds_dma16(wsc + kFacOff, (uint32_t)lane * 16, lds_addr(sl.fac));
-  };
-  // L2 prefetch of chunk c (loader wavefronts): one 4-byte load per 128-byte
-  // line of its record and of its q and k rows (the four V-slices of a head
-  // share them, every fourth line each) and of this slice's v rows, landing
-  // in a scratch LDS word.  Every thread issues exactly one (spare threads
-  // repeat a line), so the wait counts stay exact.
-  auto touch = [&](int c) {
-    constexpr int kWsLines = (int)((kChunkBytes + 127) / 128);
-    constexpr int kShared = kWsLines + 4 * C;  // + q and k rows, two lines each
-    constexpr int kPerSlice = (kShared + 3) / 4;
-    static_assert(kPerSlice + C <= 256, "one prefetch per loader thread");
-    const int t0 = c * C;
-    const int last = min(C, T - t0) - 1;
-    const uint8_t* wsc = ws + (((size_t)b * H + h) * NS + (c - c0)) * kChunkBytes;
-    const int64_t row0 = ((int64_t)b * T + t0) * tok_stride + (int64_t)h * DK;
-    const void* a;
-    const int j = min(ltid, kPerSlice - 1) * 4 + vs;
-    if (ltid < kPerSlice && j < kShared) {
-      if (j < kWsLines) {
-        a = wsc + (size_t)j * 128;
-      } else {
-        const int r = j - kWsLines;  // 4 lines per token row: q then k, two halves each
-        a = ((r & 2) ? k : q) + row0 + (int64_t)min(r >> 2, last) * tok_stride + (r & 1) * 64;
-      }
-    } else {
-      const int r = min(max(ltid - kPerSlice, 0), C - 1);
-      a = v + row0 + (int64_t)min(r, last) * tok_stride + v0;
-    }
-    asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, off" : : "v"(a), "{m0}"(lds_addr(touch_s))
-                 : "memory");
-  };
-
-  // state rows of a compute wave: d = 32 * wave + (r / 4) * 8 + half * 4 + r % 4
-  f32x16 s_acc = {};
-  if (!loader) {
+  const int l = rb * 32 + col;
+  const float gl = fc[kFacGC + l], bel = fc[kFacB + l];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int d = 32 * wave + (r >> 2) * 8 + half * 4 + (r & 3);
-      s_acc[r] = h0 ? h0[(((int64_t)b * H + h) * DK + d) * DV + v0 + col] : 0.0f;
-    }
-  }
-  auto publish_state = [&]() {
+  for (int g4 = 0; g4 < 4; ++g4) {
+    const int s0 = cb * 32 + g4 * 8 + half * 4;
+    const float4 gs4 = *reinterpret_cast<const float4*>(fc + kFacGC + s0);
+    const float gsv[4] = {gs4.x, gs4.y, gs4.z, gs4.w};
+    float val[4];
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = 32 * wave + g4 * 8 + half * 4;
-      *reinterpret_cast<uint2*>(st_s + col * SP + d) =
-          pack_bf16x4(s_acc[g4 * 4 + 0], s_acc[g4 * 4 + 1], s_acc[g4 * 4 + 2], s_acc[g4 * 4 + 3]);
+    for (int e = 0; e < 4; ++e) {
+      // branch-free: the decay is evaluated for every element (argument
+      // clamped to <= 0, exact where it is used) and selected
+      float gd = exp2f_fast(fminf((gl - gsv[e]) * kLog2e, 0.0f));
+      asm volatile("" : "+v"(gd));
+      val[e] = gd * kk[g4 * 4 + e];
     }
-  };
-  // a 32-row block of a [token][v] accumulator (rows 32 rblk + ..; lane: v
-  // column `col`) as bf16 into the transposed image [v][token], each value
-  // scaled by the factor of its token row
-  auto put_rows_t = [&](bf16* img, const f32x16& acc, const float* fac) {
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int cl = rblk * 32 + g4 * 8 + half * 4;
-      const float4 f = fac ? *reinterpret_cast<const float4*>(fac + cl)
-                           : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-      *reinterpret_cast<uint2*>(img + col * CP + cl) =
-          pack_bf16x4(acc[g4 * 4 + 0] * f.x, acc[g4 * 4 + 1] * f.y, acc[g4 * 4 + 2] * f.z,
-                      acc[g4 * 4 + 3] * f.w);
-    }
-  };
-
-  // one chunk: `cur` holds its operands (and st_s); the loader wavefronts
-  // fill `nxt` meanwhile
-  auto step = [&](int c, const ChunkSlot& cur, ChunkSlot& nxt) {
-    if (loader) {
-      // chunk c + 1 into `nxt` (past the end: the last chunk again, never
-      // read), then the L2 prefetch of chunk c + 2.  Both are unconditional
-      // so that the wait counts stay exact
-      load_rows(min(c + 1, c1 - 1), nxt);
-      lds_barrier();  // (barrier U)
-      load_record(min(c + 1, c1 - 1), nxt);
-      touch(min(c + 2, c1 - 1));
-      lds_barrier();  // (barrier W)
-      // a wavefront's counters cover only its own loads: each loader waits
-      // for its share of the next chunk's images (everything but the one
-      // prefetch issued last: vmcnt(1)) before the barrier
-      __builtin_amdgcn_s_waitcnt(0x0F71);
-      lds_barrier();  // (barrier A)
-      return;
-    }
-    const int t0 = c * C;
-    const int n = min(C, T - t0);
-
-    // waves 0, 1: P = k S (token rows 32 rblk ..), then U = v - e^{gc} o P;
-    // waves 2, 3: the output in the transposed orientation, o^T = S^T q^T
-    // (tokens 32 rblk ..), so that a lane owns one token: its row factor is
-    // one scalar and its 16 values are 4 runs of 4 consecutive v, stored
-    // straight to memory
-    f32x16 acc = {};
-    if (wave < 2) {
-#pragma unroll
-      for (int ks = 0; ks < DK / 16; ++ks)
-        acc = mfma(ld8(cur.k + swz16(arow, ks * 2 + half)),
-                   ld8(st_s + col * SP + ks * 16 + half * 8), acc);
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int cl = rblk * 32 + g4 * 8 + half * 4;
-        const float4 eg = *reinterpret_cast<const float4*>(cur.fac + kFacG + cl);
-        const uint2 vw = read_vt4(cur.v, g4);  // v[cl .. cl + 3][v0 + col]
-        const bf16* vv = reinterpret_cast<const bf16*>(&vw);
-        *reinterpret_cast<uint2*>(ut_s + col * CP + cl) =
-            pack_bf16x4(fmaf(-eg.x, acc[g4 * 4 + 0], (float)vv[0]),
-                        fmaf(-eg.y, acc[g4 * 4 + 1], (float)vv[1]),
-                        fmaf(-eg.z, acc[g4 * 4 + 2], (float)vv[2]),
-                        fmaf(-eg.w, acc[g4 * 4 + 3], (float)vv[3]));
-      }
+    if (blk == 2) {  // s < 32 <= l: no mask
+      *reinterpret_cast<uint2*>(l21 + off32(l - 32, s0 >> 3) + (s0 & 7)) =
+          pack_bf16x4(val[0], val[1], val[2], val[3]);
     } else {
 #pragma unroll
-      for (int ks = 0; ks < DK / 16; ++ks)
-        acc = mfma(ld8(st_s + col * SP + ks * 16 + half * 8),
-                   ld8(cur.q + swz16(arow, ks * 2 + half)), acc);
-      const float f = cur.fac[kFacOut + arow];  // scale e^{gc} of this lane's token
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] *= f;
+      for (int e = 0; e < 4; ++e) at[(s0 + e) * DS + col] = s0 + e < l ? bel * val[e] : 0.0f;
     }
-    lds_barrier();  // (barrier U) U^T visible
-
-    if (wave < 2) {  // W = Tu U; Tu is lower triangular: row block 0 needs tokens < 32 only
-      f32x16 wacc = {};
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ++ks) {
-        if (rblk == 0 && ks >= 2) break;
-        wacc = mfma(ld8(cur.tu + swz8(arow, ks * 2 + half)),
-                    ld8(ut_s + col * CP + ks * 16 + half * 8), wacc);
-      }
-      put_rows_t(wt_s, wacc, nullptr);
-      put_rows_t(dwt_s, wacc, cur.fac + kFacD);
-    }
-    lds_barrier();  // (barrier W) W^T and the decayed W^T visible
-
-    if (wave >= 2) {  // o^T += W^T Aqk^T, then this lane's token row to memory
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ++ks)
-        acc = mfma(ld8(wt_s + col * CP + ks * 16 + half * 8),
-                   ld8(cur.aqk + swz8(arow, ks * 2 + half)), acc);
-      if (arow < n) {
-        bf16* orow = o + ((int64_t)b * T + t0 + arow) * tok_stride + (int64_t)h * DV + v0;
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4)
-          *reinterpret_cast<uint2*>(orow + g4 * 8 + half * 4) =
-              pack_bf16x4(acc[g4 * 4 + 0], acc[g4 * 4 + 1], acc[g4 * 4 + 2], acc[g4 * 4 + 3]);
-      }
-    }
-    // S <- e^{gc_C} S + k^T (e^{gc_C - gc} o W)   (rows 32 * wave .. of the state)
-    const float dec = cur.fac[kFacChunk];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s_acc[r] *= dec;
-#pragma unroll
-    for (int ks = 0; ks < C / 16; ++ks)
-      s_acc = mfma(read_kt(cur.k, ks), ld8(dwt_s + col * CP + ks * 16 + half * 8), s_acc);
-    publish_state();
-    lds_barrier();  // (barrier A) next chunk's images, S^T and v^T visible
-  };
-
-  if (c1 > c0 && loader) {
-    load_rows(c0, slot0);
-    load_record(c0, slot0);
-    touch(min(c0 + 1, c1 - 1));
-    __builtin_amdgcn_s_waitcnt(0x0F71);
-  }
-  if (!loader) publish_state();
-  lds_barrier();
-  int c = c0;
-  for (; c + 1 < c1; c += 2) {
-    step(c, slot0, slot1);
-    step(c + 1, slot1, slot0);
-  }
-  if (c < c1) step(c, slot0, slot1);
-
-  if (loader) {
-    __builtin_amdgcn_s_waitcnt(0);  // no load may land after the workgroup's LDS is released
-    return;
-  }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int d = 32 * wave + (r >> 2) * 8 + half * 4 + (r & 3);
-    hT[(((int64_t)b * H + h) * DK + d) * DV + v0 + col] = s_acc[r];
   }
 }
 
-}  // namespace gdn
-}  // namespace tileops
+// PB (waves pw 0, 1): the diagonal 16x16 blocks 2 pw, 2 pw + 1 of T by
+// substitution (lane group (lane / 16) % 2 takes one block, lane j column
+// j; p[i] accumulates sum_m A[i][m] T[m][j]; the A columns are read four
+// steps ahead).
+__device__ __forceinline__ void prep_subst(const float* at, float* t, int pw, int lane) {
+  const int base = 16 * (2 * pw + ((lane >> 4) & 1)), jl = lane & 15;
+  const int cb = base & 31;  // column of the block inside its 32x32 block
+  float p[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) p[i] = 0.0f;
+  // av[m % 4][gq] = A[base + 4gq .. 4gq + 3][base + m], for the groups gq
+  // with a row below m
+  const float4* a4p = reinterpret_cast<const float4*>(at + base * DS + cb);
+  float4 av[4][4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int gq = (st + 1) >> 2; gq < 4; ++gq) av[st][gq] = a4p[st * (DS / 4) + gq];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const float tv = (m == jl ? 1.0f : 0.0f) - p[m];
+    // every lane writes (lane groups 0 / 2 and 1 / 3 hold the same
+    // columns, so their writes agree): no exec-masked branch in the chain
+    t[(base + m) * DS + cb + jl] = tv;
+#pragma unroll
+    for (int gq = (m + 1) >> 2; gq < 4; ++gq) {
+      const float4 a4 = av[m & 3][gq];
+      const int i4 = 4 * gq;
+      if (i4 + 0 > m) p[i4 + 0] = fmaf(a4.x, tv, p[i4 + 0]);
+      if (i4 + 1 > m) p[i4 + 1] = fmaf(a4.y, tv, p[i4 + 1]);
+      if (i4 + 2 > m) p[i4 + 2] = fmaf(a4.z, tv, p[i4 + 2]);
+      if (i4 + 3 > m) p[i4 + 3] = fmaf(a4.w, tv, p[i4 + 3]);
+    }
+    if (m + 4 < 16) {
+#pragma unroll
+      for (int gq = (m + 5) >> 2; gq < 4; ++gq) av[m & 3][gq] = a4p[(m + 4) * (DS / 4) + gq];
+    }
+  }
+}
 
-using namespace tileops;
+// PC + PF (waves pw 0, 1): in the diagonal 32x32 block pw of T, the block
+// below its diagonal 16x16 blocks, T10 = -T11 (A10 T00) (pw 0) or T32 =
+// -T33 (A32 T22) (pw 1), on v_mfma_f32_16x16x4f32 (A[mi][mk], B[mk][mi],
+// D[4 mk + r][mi]); then Tu = T diag(beta) of the block in bf16 (its upper
+// right 16x16 block is the constant zero block of t).
+__device__ __forceinline__ void prep_merge16(const float* at, float* t, float* x, const float* fc,
+                                             bf16* tu, int pw, int lane) {
+  const int mi = lane & 15, mk = lane >> 4;
+  const int d0 = 32 * pw;
+  f32x4 y = {};
+  float ya[4], yb[4], za[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int kx = 4 * kk + mk;
+    ya[kk] = at[(d0 + kx) * DS + 16 + mi];
+    yb[kk] = t[(d0 + kx) * DS + mi];
+    za[kk] = t[(d0 + 16 + mi) * DS + 16 + kx];
+  }
+  sched_fence();
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) y = __builtin_amdgcn_mfma_f32_16x16x4f32(ya[kk], yb[kk], y, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) x[(16 * pw + 4 * mk + r) * XS + mi] = y[r];
+  wave_lds_fence();
+  f32x4 z = {};
+  float zb[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) zb[kk] = x[(16 * pw + 4 * kk + mk) * XS + mi];
+  sched_fence();
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) z = __builtin_amdgcn_mfma_f32_16x16x4f32(za[kk], zb[kk], z, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) t[(d0 + 16 + 4 * mk + r) * DS + mi] = -z[r];
+  wave_lds_fence();
+  const int cg = lane & 7;  // the lane's column group in every row it converts
+  const float4 bt = *reinterpret_cast<const float4*>(fc + kFacB + d0 + 4 * cg);
+  float4 tv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    tv[i] = *reinterpret_cast<const float4*>(t + (d0 + 8 * i + (lane >> 3)) * DS + 4 * cg);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 8 * i + (lane >> 3);
+    *reinterpret_cast<uint2*>(tu + off32(row, cg >> 1) + (cg & 1) * 4) =
+        pack_bf16x4(tv[i].x * bt.x, tv[i].y * bt.y, tv[i].z * bt.z, tv[i].w * bt.w);
+  }
+}
 
-namespace tileops {
-namespace gdn {
+// Decay scan of one chunk (one wavefront): factors from the raw g | beta.
+__device__ __forceinline__ void prep_scan(const float* gbr, float* fc, int n, float scale,
+                                          int lane) {
+  float x = lane < n ? gbr[lane] : 0.0f;
+  const float bt = lane < n ? gbr[C + lane] : 0.0f;
+  x = wave_inclusive_sum(x);  // gc
+  const float gl =
+      __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), C - 1));
+  const float eg = exp2f_fast(x * kLog2e);
+  fc[kFacSE + lane] = scale * eg;
+  fc[kFacE + lane] = eg;
+  fc[kFacD + lane] = exp2f_fast((gl - x) * kLog2e);
+  fc[kFacGC + lane] = x;
+  fc[kFacB + lane] = bt;
+  if (lane == 0) fc[kFacEG] = exp2f_fast(gl * kLog2e);
+}
 
-// Workspace bytes for `nchunks` chunks of each of B * H heads.
-inline size_t records_bytes(int64_t BH, int64_t nchunks) {
-  return (size_t)(BH * nchunks) * kChunkBytes;
+// ---------------------------------------------------------------------------
+// The chain wavefronts: NB blocks of 16 state columns each
+// ---------------------------------------------------------------------------
+// State: s[nb][kb][r] (lane group g, lane ln = lane % 16) holds
+// S[acc_row(kb, g, r)][col0 + 16 nb + ln].
+template <int NB>
+__device__ __forceinline__ void state_load(f32x4 (&s)[NB][8], const float* src, int col0, int g,
+                                           int ln) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        s[nb][kb][r] = src ? src[acc_row(kb, g, r) * DV + col0 + 16 * nb + ln] : 0.0f;
+}
+template <int NB>
+__device__ __forceinline__ void state_store(const f32x4 (&s)[NB][8], float* dst, int col0, int g,
+                                            int ln) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[acc_row(kb, g, r) * DV + col0 + 16 * nb + ln] = s[nb][kb][r];
+}
+
+// x as bf16 hi + lo (x - hi rounded again): a sum of the three products
+// hi*hi + hi*lo + lo*hi carries ~16 significant bits.
+__device__ __forceinline__ void split8(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
+  hi = pack8(a, b);
+  f32x4 ra, rb;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    ra[e] = a[e] - (float)hi[e];
+    rb[e] = b[e] - (float)hi[4 + e];
+  }
+  lo = pack8(ra, rb);
+}
+
+// s <- Phi s + Bseg for this wavefront's columns (Bseg K x DV and Phi K x K,
+// fp32 row-major), one column block at a time.
+template <int NB>
+__device__ __forceinline__ void state_compose(f32x4 (&s)[NB][8], const float* phi,
+                                              const float* bseg, int col0, int g, int ln) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    bf16x8 bh[4], bl[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) split8(s[nb][2 * ks], s[nb][2 * ks + 1], bh[ks], bl[ks]);
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+      f32x4 acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = bseg[acc_row(kb, g, r) * DV + col0 + 16 * nb + ln];
+      const float* prow = phi + lam(kb, ln) * DK + 8 * g;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const float4 x0 = *reinterpret_cast<const float4*>(prow + 32 * ks);
+        const float4 x1 = *reinterpret_cast<const float4*>(prow + 32 * ks + 4);
+        bf16x8 ah, al;
+        split8(f32x4{x0.x, x0.y, x0.z, x0.w}, f32x4{x1.x, x1.y, x1.z, x1.w}, ah, al);
+        acc = mfma16(ah, bh[ks], acc);
+        acc = mfma16(ah, bl[ks], acc);
+        acc = mfma16(al, bh[ks], acc);
+      }
+      s[nb][kb] = acc;
+    }
+  }
+}
+
+// k^T as the A operand of S' for key block kb and token step ts: lane-row m
+// = ln holds key lam(kb, ln), k-slots 8 g + e tokens 32 ts + 8 g + e.
+__device__ __forceinline__ bf16x8 read_kt(const bf16* kimg, int kb, int ts, int g, int ln) {
+  const int chunk = 4 * (kb >> 1) + (ln & 3);
+  const int within = 4 * (kb & 1);
+  const int row = 32 * ts + 8 * g + (ln >> 2);
+  const v4i16 x0 = ds_read_tr(kimg + off128(row, chunk) + within);
+  const v4i16 x1 = ds_read_tr(kimg + off128(row + 4, chunk) + within);
+  const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
+  const u32x4 w4 = {y0.x, y0.y, y1.x, y1.y};
+  return __builtin_bit_cast(bf16x8, w4);
+}
+
+// v of tokens t0 .. t0 + 3 at column c0 + ln (c0 a multiple of 16).
+__device__ __forceinline__ f32x4 read_v4(const bf16* vimg, int t0, int c0, int ln) {
+  const int colw = c0 + 4 * (ln & 3);
+  const v4i16 x = ds_read_tr(vimg + off128(t0 + (ln >> 2), colw >> 3) + (colw & 7));
+  const bf16* b = reinterpret_cast<const bf16*>(&x);
+  return f32x4{(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+}
+
+// Values a chain wavefront carries from the first part of a chunk step to
+// the second.
+template <int NB>
+struct ChainTmp {
+  f32x4 u[NB][4];  // U (accumulator rows acc_row)
+  f32x4 o[NB][4];  // o^T: rows columns 16 nb + 4 g + r, column token 16 tb + ln
+};
+
+// Part 1, from S at the chunk start: P = k S (exact segments also o^T =
+// scale e^{gc} o (S^T q^T)), then U = v - e^{gc} o P (v = 0 for Phi
+// columns).
+template <int NB, bool OUT>
+__device__ __forceinline__ void chain_part1(const f32x4 (&s)[NB][8], ChainTmp<NB>& t,
+                                            const bf16* kimg, const bf16* vimg, const bf16* qimg,
+                                            const float* fc, bool usev, int col0, int g, int ln) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) t.u[nb][tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (OUT) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) t.o[nb][tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  // P and o^T share the bf16 state operands; the k and q rows of key step
+  // ks + 1 are read while the MFMAs of step ks run
+  bf16x8 a[2][4], b[2][4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    a[0][tb] = ld8(kimg + off128(lam(tb, ln), g));
+    if constexpr (OUT) b[0][tb] = ld8(qimg + off128(16 * tb + ln, g));
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks < 3) {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        a[(ks + 1) & 1][tb] = ld8(kimg + off128(lam(tb, ln), 4 * (ks + 1) + g));
+        if constexpr (OUT)
+          b[(ks + 1) & 1][tb] = ld8(qimg + off128(16 * tb + ln, 4 * (ks + 1) + g));
+      }
+    }
+    sched_fence();
+    bf16x8 sb[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) sb[nb] = pack8(s[nb][2 * ks], s[nb][2 * ks + 1]);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        t.u[nb][tb] = mfma16(a[ks & 1][tb], sb[nb], t.u[nb][tb]);
+        if constexpr (OUT) t.o[nb][tb] = mfma16(sb[nb], b[ks & 1][tb], t.o[nb][tb]);
+      }
+  }
+  f32x4 vv[NB][4], ev[4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int t0 = acc_row(tb, g, 0);
+    const float4 e4 = *reinterpret_cast<const float4*>(fc + kFacE + t0);
+    ev[tb] = f32x4{e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      vv[nb][tb] = usev ? read_v4(vimg, t0, col0 + 16 * nb, ln) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  sched_fence();
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        t.u[nb][tb][r] = fmaf(-ev[tb][r], t.u[nb][tb][r], vv[nb][tb][r]);
+  if constexpr (OUT) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const float f = fc[kFacSE + 16 * tb + ln];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) t.o[nb][tb][r] *= f;
+    }
+  }
+}
+
+// Aqk block bi of the current chunk, in 32x32 blocks (tb, sb) = (0,0)
+// (1,0) (1,1): D = k_blk q_blk^T on 32x32x16 MFMA (a lane owns token t = 32
+// tb + lane % 32, its 16 values run over s), masked (s <= t), decayed and
+// scaled, stored as 4 consecutive s of row t.  The blocks above are constant
+// zero.
+__device__ __forceinline__ void aqk_block(int bi, const bf16* kimg, const bf16* qimg,
+                                          const float* fc, bf16* aqk, float scale, int lane) {
+  const int tb = bi == 0 ? 0 : 1, sb = bi == 2 ? 1 : 0;
+  const int col = lane & 31, half = lane >> 5;
+  f32x16 d = {};
+  bf16x8 a[4], b[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ks = 4 * h + i;
+      a[i] = ld8(kimg + off128(32 * sb + col, 2 * ks + half));
+      b[i] = ld8(qimg + off128(32 * tb + col, 2 * ks + half));
+    }
+    sched_fence();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d = mfma32(a[i], b[i], d);
+  }
+  const int t = 32 * tb + col;
+  const float gt = fc[kFacGC + t];
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4) {
+    const int s0 = 32 * sb + 8 * g4 + 4 * half;
+    const float4 gs4 = *reinterpret_cast<const float4*>(fc + kFacGC + s0);
+    const float gsv[4] = {gs4.x, gs4.y, gs4.z, gs4.w};
+    float val[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float gd = exp2f_fast(fminf((gt - gsv[e]) * kLog2e, 0.0f));
+      asm volatile("" : "+v"(gd));
+      val[e] = s0 + e <= t ? scale * gd * d[4 * g4 + e] : 0.0f;
+    }
+    *reinterpret_cast<uint2*>(aqk + off64(t, s0 >> 3) + (s0 & 7)) =
+        pack_bf16x4(val[0], val[1], val[2], val[3]);
+  }
+}
+
+// Part 2: W_top = Tu11 U_top, W_bot = Tu22 (U_bot - L21 W_top); exact
+// segments o^T += W^T Aqk^T and store o; then
+// S <- e^{gamma} S + k^T (e^{gamma - gc} o W).  DEEP: k^T read two key
+// blocks ahead (256-register wavefronts), else one.
+template <int NB, bool OUT, bool DEEP>
+__device__ __forceinline__ void chain_part2(f32x4 (&s)[NB][8], ChainTmp<NB>& t, const bf16* kimg,
+                                            const bf16* tu11, const bf16* tu22, const bf16* l21,
+                                            const bf16* aqkimg, const float* fc, bf16* orow0,
+                                            int64_t otok, int n, int col0, int g, int ln) {
+  bf16x8 wa[2], wl[2], wz[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    wa[j] = ld8(tu11 + off32(lam(j, ln), g));
+    wl[j] = ld8(l21 + off32(lam(2 + j, ln) - 32, g));
+    wz[j] = ld8(tu22 + off32(lam(2 + j, ln) - 32, g));
+  }
+  constexpr int KD = DEEP ? 3 : 2;  // k^T ring
+  bf16x8 ka[KD][2];
+#pragma unroll
+  for (int j = 0; j < KD - 1; ++j)
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts) ka[j][ts] = read_kt(kimg, j, ts, g, ln);
+  bf16x8 b[6];  // Aqk rows: (tb, ss) = (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
+  if constexpr (OUT) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int tb = i < 2 ? i : 2 + ((i - 2) >> 1), ss = i < 2 ? 0 : (i - 2) & 1;
+      b[i] = ld8(aqkimg + off64(16 * tb + ln, 4 * ss + g));
+    }
+  }
+  sched_fence();
+  f32x4 w[NB][4];
+  // W_top = Tu11 U_top (token blocks 0, 1; one 32-token step)
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const bf16x8 ut = pack8(t.u[nb][0], t.u[nb][1]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) w[nb][j] = mfma16(wa[j], ut, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+  }
+  // W_bot = Tu22 (U_bot - L21 W_top) (token blocks 2, 3)
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const bf16x8 wt = pack8(w[nb][0], w[nb][1]);
+    f32x4 r2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) r2[j] = mfma16(wl[j], wt, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+    for (int j = 0; j < 2; ++j) r2[j] = t.u[nb][2 + j] - r2[j];
+    const bf16x8 rb = pack8(r2[0], r2[1]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) w[nb][2 + j] = mfma16(wz[j], rb, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+  }
+  bf16x8 wb[NB][2], dwb[NB][2];
+#pragma unroll
+  for (int ss = 0; ss < 2; ++ss) {
+    const float4 d0 = *reinterpret_cast<const float4*>(fc + kFacD + 32 * ss + 8 * g);
+    const float4 d1 = *reinterpret_cast<const float4*>(fc + kFacD + 32 * ss + 8 * g + 4);
+    const f32x4 dv0 = {d0.x, d0.y, d0.z, d0.w}, dv1 = {d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if constexpr (OUT) wb[nb][ss] = pack8(w[nb][2 * ss], w[nb][2 * ss + 1]);
+      dwb[nb][ss] = pack8(w[nb][2 * ss] * dv0, w[nb][2 * ss + 1] * dv1);
+    }
+  }
+  if constexpr (OUT) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+      for (int ss = 0; ss <= (tb >> 1); ++ss) {
+        const int i = tb < 2 ? tb : 2 + 2 * (tb - 2) + ss;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) t.o[nb][tb] = mfma16(wb[nb][ss], b[i], t.o[nb][tb]);
+      }
+      const int tok = 16 * tb + ln;
+      if (tok < n) {
+        bf16* orow = orow0 + (int64_t)tok * otok + col0 + 4 * g;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          *reinterpret_cast<uint2*>(orow + 16 * nb) = pack_bf16x4(
+              t.o[nb][tb][0], t.o[nb][tb][1], t.o[nb][tb][2], t.o[nb][tb][3]);
+      }
+    }
+  }
+  const float eg = fc[kFacEG];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) s[nb][kb] *= eg;
+#pragma unroll
+  for (int kb = 0; kb < 8; ++kb) {
+    if (kb + KD - 1 < 8) {
+#pragma unroll
+      for (int ts = 0; ts < 2; ++ts)
+        ka[(kb + KD - 1) % KD][ts] = read_kt(kimg, kb + KD - 1, ts, g, ln);
+    }
+    sched_fence();
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) s[nb][kb] = mfma16(ka[kb % KD][ts], dwb[nb][ts], s[nb][kb]);
+  }
+}
+
+// Geometry of one workgroup's segment.
+struct Seg {
+  int b, h, bh;
+  int seg;      // segment index
+  bool exact;   // exact segment (outputs) or map segment
+  int c0, nch;  // first chunk, chunk count
+};
+
+__device__ __forceinline__ float* ws_slot(const Args& A, int bh, int idx) {
+  const int nslot = 2 * A.nseg - 3;
+  return A.ws + ((size_t)bh * nslot + idx) * kStateFloats;
+}
+
+// Chain wavefront program.  Every wavefront of the workgroup passes the same
+// barrier sequence: 4 in the prologue, 2 per chunk.
+template <int NB, bool OUT, bool DEEP>
+__device__ void run_chain(const Args& A, Smem& sm, const Seg& sg, int wave, bool idle, int lane) {
+  const int g = lane >> 4, ln = lane & 15;
+  const int64_t tok_stride = (int64_t)A.H * DK;
+  // columns: exact segments 16 NB wave ..; map segments: waves 0-3 value
+  // columns 32 wave .., waves 4-7 Phi columns 32 (wave - 4) ..
+  const bool usev = OUT || wave < 4;
+  const int col0 = OUT ? 16 * NB * wave : 32 * (wave & 3);
+  f32x4 s[NB][8];
+  ChainTmp<NB> tmp;
+  if (!idle) {
+    if (OUT) {
+      if (sg.seg == 0) {
+        state_load<NB>(s, A.h0 ? A.h0 + (size_t)sg.bh * kStateFloats : nullptr, col0, g, ln);
+      } else {
+        state_load<NB>(s, ws_slot(A, sg.bh, 0), col0, g, ln);
+        for (int j = 1; j < sg.seg; ++j)
+          state_compose<NB>(s, ws_slot(A, sg.bh, 1 + 2 * (j - 1)),
+                            ws_slot(A, sg.bh, 2 + 2 * (j - 1)), col0, g, ln);
+      }
+    } else if (usev) {
+      state_load<NB>(s, nullptr, col0, g, ln);
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            s[nb][kb][r] = acc_row(kb, g, r) == col0 + 16 * nb + ln ? 1.0f : 0.0f;
+    }
+  }
+  // prologue: loads (P0), scans (P1), chunk 0's products (P2) and
+  // diagonal blocks of T (P3)
+  for (int i = 0; i < 4; ++i) lds_barrier();
+
+  for (int c = 0; c < sg.nch; ++c) {
+    const int cg = sg.c0 + c;
+    const int n = min(C, A.T - cg * C);
+    const bf16* kimg = sm.k[c % 3];
+    const bf16* qimg = sm.q[c & 1];
+    const float* fc = sm.fac[c % 3];
+    if (!idle) {
+      const int l1 = opaque(lane);
+      chain_part1<NB, OUT>(s, tmp, kimg, sm.v, qimg, fc, usev, col0, l1 >> 4, l1 & 15);
+      if constexpr (OUT) {
+        if (wave < 3) aqk_block(wave, kimg, qimg, fc, sm.aqk, A.scale, opaque(lane));
+      }
+      // with four chain wavefronts, wave 3 (no Aqk block) also forms L21 of
+      // the next chunk
+      if constexpr (DEEP) {
+        if (wave == 3 && c + 1 < sg.nch)
+          prep_products<4>(sm.k[(c + 1) % 3], sm.fac[(c + 1) % 3], nullptr, sm.l21[(c + 1) & 1],
+                           2, opaque(lane));
+      }
+    }
+    lds_barrier();
+    if (!idle) {
+      const int l2 = opaque(lane);
+      bf16* orow0 =
+          A.o + ((int64_t)sg.b * A.T + (int64_t)cg * C) * tok_stride + (int64_t)sg.h * DV;
+      chain_part2<NB, OUT, DEEP>(s, tmp, kimg, sm.tu[0], sm.tu[1], sm.l21[c & 1], sm.aqk, fc,
+                                 orow0, tok_stride, n, col0, l2 >> 4, l2 & 15);
+    }
+    lds_barrier();
+  }
+  if (idle) return;
+  float* dst;
+  if (OUT) {
+    if (sg.seg == A.nseg - 1)
+      dst = A.hT + (size_t)sg.bh * kStateFloats;
+    else if (sg.seg == 0)
+      dst = ws_slot(A, sg.bh, 0);  // segment 0's end state for the composition
+    else
+      return;  // an inner exact segment: its end state is not needed
+  } else {
+    dst = ws_slot(A, sg.bh, (usev ? 2 : 1) + 2 * (sg.seg - 1));
+  }
+  state_store<NB>(s, dst, col0, g, ln);
+}
+
+// Prep wavefront program (pw = wave - NCW).
+template <int NCW>
+__device__ void run_prep(const Args& A, Smem& sm, const Seg& sg, int pw, int lane) {
+  constexpr bool kDeep = NCW == 4;
+  const int64_t tok_stride = (int64_t)A.H * DK;
+  const int lw = pw - 2;  // half of the loads that prep waves 2, 3 issue together (v, prologue)
+  const bool exact = sg.exact;
+  auto rows0 = [&](int c) {  // element offset of the chunk's first token row of head h
+    return ((int64_t)sg.b * A.T + (int64_t)(sg.c0 + c) * C) * tok_stride + (int64_t)sg.h * DK;
+  };
+  auto nrows = [&](int c) { return min(C, A.T - (sg.c0 + c) * C); };
+  // loads of one chunk's images, the half h (0, 1) of their 1 KB windows
+  auto load_k = [&](int c, int h) {
+    if (c < sg.nch) fill128(sm.k[c % 3], A.k + rows0(c), tok_stride, nrows(c) - 1, h, lane);
+  };
+  auto load_q = [&](int c, int h) {
+    if (exact && c < sg.nch)
+      fill128(sm.q[c & 1], A.q + rows0(c), tok_stride, nrows(c) - 1, h, lane);
+  };
+  auto load_v = [&](int c, int h) {
+    if (c < sg.nch) fill128(sm.v, A.v + rows0(c), tok_stride, nrows(c) - 1, h, lane);
+  };
+  auto load_gb = [&](int c, int h) {  // h 0: g, 1: beta
+    if (c < sg.nch) {
+      const int n = nrows(c);
+      const int64_t gi =
+          ((int64_t)sg.b * A.T + (int64_t)(sg.c0 + c) * C + min(lane, n - 1)) * A.H + sg.h;
+      lds_dma4((h == 0 ? A.g : A.beta) + gi, lds_addr(sm.gb[c & 3] + h * C));
+    }
+  };
+  auto scan = [&](int c) {
+    if (c < sg.nch) prep_scan(sm.gb[c & 3], sm.fac[c % 3], nrows(c), A.scale, lane);
+  };
+
+  // ---- prologue
+  if (pw >= 2) {
+    load_k(0, lw);
+    load_k(1, lw);
+    load_q(0, lw);
+    load_v(0, lw);
+    load_gb(0, lw);
+    load_gb(1, lw);
+    load_gb(2, lw);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  } else {
+    // constant zeros, in 8-byte groups: the Aqk blocks (tb, sb) with sb > tb
+    // (16-row blocks)
+    for (int e = 64 * pw + lane; e < 384; e += 128) {
+      const int blk = e >> 6, i = e & 63;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+      const int tb = blk < 3 ? 0 : blk < 5 ? 1 : 2;
+      const int sb = tb == 0 ? 1 + blk : tb == 1 ? blk - 1 : 3;
+      const int arow = 16 * tb + (i >> 2), acg = 4 * sb + (i & 3);
+      *reinterpret_cast<uint2*>(sm.aqk + off64(arow, acg >> 1) + (acg & 1) * 4) =
+          make_uint2(0u, 0u);
+    }
+    // T above its diagonal 16x16 blocks inside the 32x32 ones (T01, T23),
+    // read as part of Tu11 / Tu22
+    for (int e = 64 * pw + lane; e < 512; e += 128) {
+      const int blk = e >> 8, i = e & 255;
+      sm.t[(32 * blk + (i >> 4)) * DS + 16 + (i & 15)] = 0.0f;
+    }
+  }
+  lds_barrier();  // P0
+  if (pw == 3) {
+    scan(0);
+    scan(1);
+  }
+  lds_barrier();  // P1
+  if (pw < 3) prep_products<kDeep ? 8 : 4>(sm.k[0], sm.fac[0], sm.at[0], sm.l21[0], pw, lane);
+  lds_barrier();  // P2
+  if (pw < 2) prep_subst(sm.at[0], sm.t, pw, lane);
+  lds_barrier();  // P3
+
+  for (int c = 0; c < sg.nch; ++c) {
+    const bool more = c + 1 < sg.nch;
+    // part 1: waves 0, 1 load half each of k (c + 2), q (c + 1) and g | beta
+    // (c + 3), then finish T and Tu of chunk c (their 32x32 halves); waves 2,
+    // 3 form the diagonal product blocks of c + 1 (chain wave 3 forms L21)
+    if (pw < 2) {
+      load_k(c + 2, pw);
+      load_q(c + 1, pw);
+      load_gb(c + 3, pw);
+      prep_merge16(sm.at[c & 1], sm.t, sm.x, sm.fac[c % 3], sm.tu[pw], pw, opaque(lane));
+    } else if (more) {
+      prep_products<kDeep ? 8 : 4>(sm.k[(c + 1) % 3], sm.fac[(c + 1) % 3], sm.at[(c + 1) & 1],
+                                   nullptr, pw - 2, opaque(lane));
+      if (!kDeep && pw == 2)  // eight chain wavefronts: L21 here
+        prep_products<4>(sm.k[(c + 1) % 3], sm.fac[(c + 1) % 3], nullptr, sm.l21[(c + 1) & 1], 2,
+                         opaque(lane));
+    }
+    lds_barrier();
+    // part 2: diagonal blocks of T of c + 1; v of c + 1 (chunk c's U is
+    // formed); factors of c + 2
+    if (pw < 2 && more) prep_subst(sm.at[(c + 1) & 1], sm.t, pw, opaque(lane));
+    if (pw >= 2) load_v(c + 1, lw);
+    if (pw == 3) scan(c + 2);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's loads have landed
+    lds_barrier();
+  }
+}
+
+template <int NCW>
+__global__ __launch_bounds__(64 * (NCW + 4)) void gdn_fused_kernel(Args A) {
+  constexpr int TNB = 8 / NCW;
+  __shared__ __attribute__((aligned(16))) Smem sm;
+  // wave-uniform in SGPRs: role branches and pointer choices stay scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int BH = A.B * A.H;
+  Seg sg;
+  sg.bh = blockIdx.x % BH;
+  const int sidx = blockIdx.x / BH;
+  sg.seg = A.phase == 1 ? sidx : sidx + 1;
+  sg.exact = A.phase == 2 || sg.seg == 0;
+  sg.b = sg.bh / A.H;
+  sg.h = sg.bh % A.H;
+  sg.c0 = A.start[sg.seg];
+  sg.nch = A.start[sg.seg + 1] - sg.c0;
+  if (wave >= NCW) {
+    run_prep<NCW>(A, sm, sg, wave - NCW, lane);
+  } else if (sg.exact) {
+    run_chain<TNB, true, NCW == 4>(A, sm, sg, wave, false, lane);
+  } else if constexpr (NCW == 8) {
+    run_chain<2, false, false>(A, sm, sg, wave, false, lane);
+  }
+}
+
+// State pass-through for T = 0: hT = h0 (or 0).
+__global__ __launch_bounds__(256) void gdn_copy_state_kernel(const float* h0, float* hT,
+                                                             int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) hT[i] = h0 ? h0[i] : 0.0f;
+}
+
+// Segment count: enough (head, segment) workgroups for the device's compute
+// units in each launch (one workgroup per CU: its LDS images fill one), at
+// least 4 chunks per segment, and none when the heads alone fill the device.
+static int plan_segments(int64_t BH, int64_t nc, int requested) {
+  int ns;
+  if (requested > 0) {
+    ns = (int)std::min<int64_t>(std::min<int64_t>(requested, kMaxSeg), std::max<int64_t>(nc, 1));
+  } else {
+    const int cus = device_cu_count();
+    if (nc < 8 || 2 * BH > cus) return 1;
+    ns = (int)std::min<int64_t>(std::min<int64_t>(cus / BH + 1, nc / 4), kMaxSeg);
+    if (ns < 3) ns = 1;
+  }
+  return std::max(ns, 1);
+}
+
+inline size_t ws_bytes_for(int64_t BH, int nseg) {
+  return nseg <= 1 ? 0 : (size_t)BH * (size_t)(2 * nseg - 3) * kStateFloats * sizeof(float);
 }
 
 // Argument checks shared by the entry points (0 when the call may proceed).
@@ -779,77 +1022,135 @@ static int check_args(const void* q, const void* k, const void* v, const float* 
   if (B < 0 || T < 0 || H <= 0) return TILEOPS_ESHAPE;
   if (K != DK || V != DV || chunk != C) return TILEOPS_ESHAPE;
   if (B > 65535 || H > 65535 || T > INT32_MAX / 2) return TILEOPS_ESHAPE;
+  if (B * H * (int64_t)kMaxSeg > INT32_MAX) return TILEOPS_ESHAPE;
   if (dtype != TILEOPS_BF16) return TILEOPS_EINVAL;
   if (B == 0) return 0;
   if (!hT) return TILEOPS_ENULL;
   if (T > 0) {
     if (!q || !k || !v || !g || !beta || !o) return TILEOPS_ENULL;
-    if (!host_aligned16(q) || !host_aligned16(k) || !host_aligned16(v)) return TILEOPS_EINVAL;
+    if (!host_aligned16(q) || !host_aligned16(k) || !host_aligned16(v) || !host_aligned16(o))
+      return TILEOPS_EINVAL;
   }
-  const int64_t nc = (T + C - 1) / C;
-  if (B * H * nc > (int64_t)UINT32_MAX || B * H * (DV / VS) > INT32_MAX) return TILEOPS_ESHAPE;
   return 0;
 }
 
-// The whole prefill in segments of `seg` chunks: per segment the parallel
-// preparation into `ws` (records of seg chunks per head), then the
-// recurrence over the segment, the state carried from one segment to the
-// next in hT.  One segment when `ws` holds every chunk's record.
-static int run_segments(const bf16* q, const bf16* k, const bf16* v, const float* g,
-                        const float* beta, const float* h0, bf16* o, float* hT, int B, int T,
-                        int H, float scale, uint8_t* ws, int seg, hipStream_t s) {
-  const int nc = (T + C - 1) / C;
-  const unsigned rgrid = (unsigned)(B * H * (DV / VS));
-  if (nc == 0) {  // no chunk: the state passes through
-    gdn_recur_kernel<<<dim3(rgrid), dim3(512), 0, s>>>(q, k, v, h0, ws, o, hT, B, T, H, 0, 0, 1);
+// The prefill in `nseg` segments (workspace `ws` of ws_bytes_for(BH, nseg)).
+static int run(const bf16* q, const bf16* k, const bf16* v, const float* g, const float* beta,
+               const float* h0, bf16* o, float* hT, int B, int T, int H, float scale, float* ws,
+               int nseg, hipStream_t s) {
+  const int64_t BH = (int64_t)B * H;
+  if (T == 0) {
+    const int64_t n = BH * (int64_t)kStateFloats;
+    gdn_copy_state_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(h0, hT, n);
     return launch_status();
   }
-  for (int c0 = 0; c0 < nc; c0 += seg) {
-    const int ns = std::min(seg, nc - c0);
-    const int64_t nblk = (int64_t)B * H * ns;
-    gdn_prep_kernel<<<dim3((unsigned)std::min<int64_t>(nblk, 2 * device_cu_count())), dim3(256),
-                      0, s>>>(q, k, g, beta, ws, B, T, H, c0, ns, scale);
-    gdn_recur_kernel<<<dim3(rgrid), dim3(512), 0, s>>>(q, k, v, c0 == 0 ? h0 : hT, ws, o, hT, B,
-                                                      T, H, c0, c0 + ns, ns);
-    if (int e = launch_status()) return e;
+  const int nc = (T + C - 1) / C;
+  Args a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.g = g;
+  a.beta = beta;
+  a.h0 = h0;
+  a.o = o;
+  a.hT = hT;
+  a.ws = ws;
+  a.B = B;
+  a.T = T;
+  a.H = H;
+  a.scale = scale;
+  a.nseg = nseg;
+  for (int i = 0; i <= kMaxSeg; ++i) a.start[i] = nc;
+  for (int i = 0; i < nseg; ++i) a.start[i] = (int)((int64_t)i * nc / nseg);
+  const unsigned grid = (unsigned)(BH * std::max(nseg - 1, 1));
+  if (nseg == 1) {  // every chunk exact, from h0
+    a.phase = 1;
+    gdn_fused_kernel<4><<<dim3(grid), dim3(64 * 8), 0, s>>>(a);
+    return launch_status();
   }
-  return 0;
+  a.phase = 1;
+  gdn_fused_kernel<8><<<dim3(grid), dim3(64 * 12), 0, s>>>(a);
+  if (int e = launch_status()) return e;
+  a.phase = 2;
+  gdn_fused_kernel<4><<<dim3(grid), dim3(64 * 8), 0, s>>>(a);
+  return launch_status();
 }
 
-// Scratch of the allocation-free entry point: every call on a GPU shares
-// that GPU's copy (the last call's records stay in it), so calls that
-// overlap on one GPU race.  kScratchBytes bounds the heads per call: one
-// chunk record per head must fit, B * H <= 963.
-constexpr size_t kScratchBytes = (size_t)16 << 20;
+// Scratch of the allocation-free entry point: one array per GPU, holding
+// the segment maps of the call in flight.  kScratchBytes bounds the
+// segments: B * H * (2 N - 3) states of 64 KiB must fit (N = 1 needs none).
+constexpr size_t kScratchBytes = (size_t)32 << 20;
 __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
-// Device address of `scratch` on the current device, looked up once per
-// device: in host code the array's name is only a stand-in symbol.
-static int scratch_ptr(uint8_t** out) {
+struct DeviceScratch {
+  float* ptr = nullptr;
+  hipEvent_t last = nullptr;  // completion of the previous call that used the array
+  bool recorded = false;
+};
+
+// Device address of `scratch` on the current device (looked up once per
+// device: in host code the array's name is only a stand-in symbol) and the
+// event that orders the calls using it.
+static int scratch_of(DeviceScratch** out) {
   static std::mutex mu;
-  static uint8_t* ptrs[64] = {};
+  static DeviceScratch per_dev[64];
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= 64) return TILEOPS_EINVAL;
   std::lock_guard<std::mutex> lock(mu);
-  if (!ptrs[dev]) {
+  DeviceScratch& d = per_dev[dev];
+  if (!d.ptr) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return (int)e;
-    ptrs[dev] = static_cast<uint8_t*>(p);
+    e = hipEventCreateWithFlags(&d.last, hipEventDisableTiming);
+    if (e != hipSuccess) return (int)e;
+    d.ptr = static_cast<float*>(p);
   }
-  *out = ptrs[dev];
+  *out = &d;
   return 0;
 }
 
 }  // namespace gdn
 }  // namespace tileops
 
+using namespace tileops;
+
+extern "C" size_t tileops_gdn_prefill_workspace_bytes_ex(int64_t B, int64_t T, int64_t H,
+                                                         int64_t K, int64_t V, int64_t chunk,
+                                                         int64_t segments) {
+  if (B < 0 || T < 0 || H < 0 || K != gdn::DK || V != gdn::DV || chunk != gdn::C) return 0;
+  if (B == 0 || H == 0 || T == 0 || segments < 0 || segments > gdn::kMaxSeg) return 0;
+  const int64_t nc = (T + gdn::C - 1) / gdn::C;
+  return gdn::ws_bytes_for(B * H, gdn::plan_segments(B * H, nc, (int)segments));
+}
+
 extern "C" size_t tileops_gdn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K,
                                                       int64_t V, int64_t chunk) {
-  if (B < 0 || T < 0 || H < 0 || K != gdn::DK || V != gdn::DV || chunk != gdn::C) return 0;
-  return gdn::records_bytes(B * H, (T + gdn::C - 1) / gdn::C);
+  return tileops_gdn_prefill_workspace_bytes_ex(B, T, H, K, V, chunk, 0);
+}
+
+extern "C" int tileops_gdn_prefill_fwd_ex(const void* q, const void* k, const void* v,
+                                          const float* g, const float* beta, const float* h0,
+                                          void* o, float* hT, int64_t B, int64_t T, int64_t H,
+                                          int64_t K, int64_t V, int64_t chunk, float scale,
+                                          int dtype, int64_t segments, void* ws, size_t ws_bytes,
+                                          void* stream) {
+  if (int e = gdn::check_args(q, k, v, g, beta, o, hT, B, T, H, K, V, chunk, dtype)) return e;
+  if (segments < 0 || segments > gdn::kMaxSeg) return TILEOPS_ESHAPE;
+  if (B == 0) return 0;
+  const int64_t nc = (T + gdn::C - 1) / gdn::C;
+  const int nseg = T > 0 ? gdn::plan_segments(B * H, nc, (int)segments) : 1;
+  const size_t need = gdn::ws_bytes_for(B * H, nseg);
+  if (need > 0) {
+    if (ws && !host_aligned16(ws)) return TILEOPS_EINVAL;
+    if (!ws || ws_bytes < need) return TILEOPS_EWORKSPACE;
+  }
+  return gdn::run(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                  static_cast<const bf16*>(v), g, beta, h0, static_cast<bf16*>(o), hT, (int)B,
+                  (int)T, (int)H, scale, static_cast<float*>(ws), nseg,
+                  static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tileops_gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* g,
@@ -857,18 +1158,8 @@ extern "C" int tileops_gdn_prefill_fwd(const void* q, const void* k, const void*
                                        int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
                                        int64_t chunk, float scale, int dtype, void* ws,
                                        size_t ws_bytes, void* stream) {
-  if (int e = gdn::check_args(q, k, v, g, beta, o, hT, B, T, H, K, V, chunk, dtype)) return e;
-  if (B == 0) return 0;
-  const size_t need = tileops_gdn_prefill_workspace_bytes(B, T, H, K, V, chunk);
-  if (T > 0 && (!ws || ws_bytes < need || !host_aligned16(ws))) {
-    if (ws && !host_aligned16(ws)) return TILEOPS_EINVAL;
-    return TILEOPS_EWORKSPACE;
-  }
-  const int nc = (int)((T + gdn::C - 1) / gdn::C);
-  return gdn::run_segments(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                           static_cast<const bf16*>(v), g, beta, h0, static_cast<bf16*>(o), hT,
-                           (int)B, (int)T, (int)H, scale, static_cast<uint8_t*>(ws),
-                           nc > 0 ? nc : 1, static_cast<hipStream_t>(stream));
+  return tileops_gdn_prefill_fwd_ex(q, k, v, g, beta, h0, o, hT, B, T, H, K, V, chunk, scale,
+                                    dtype, 0, ws, ws_bytes, stream);
 }
 
 extern "C" int tileops_gdn_prefill_fwd_noalloc(const void* q, const void* k, const void* v,
@@ -879,14 +1170,39 @@ extern "C" int tileops_gdn_prefill_fwd_noalloc(const void* q, const void* k, con
                                                void* stream) {
   if (int e = gdn::check_args(q, k, v, g, beta, o, hT, B, T, H, K, V, chunk, dtype)) return e;
   if (B == 0) return 0;
-  const int64_t per_chunk = B * H * (int64_t)gdn::kChunkBytes;  // one chunk of every head
-  if (T > 0 && per_chunk > (int64_t)gdn::kScratchBytes) return TILEOPS_EWORKSPACE;
-  uint8_t* ws = nullptr;
-  if (int e = gdn::scratch_ptr(&ws)) return e;
-  const int nc = (int)((T + gdn::C - 1) / gdn::C);
-  const int seg = (int)std::min<int64_t>(std::max(nc, 1), (int64_t)gdn::kScratchBytes / per_chunk);
-  return gdn::run_segments(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                           static_cast<const bf16*>(v), g, beta, h0, static_cast<bf16*>(o), hT,
-                           (int)B, (int)T, (int)H, scale, ws, seg,
-                           static_cast<hipStream_t>(stream));
+  const int64_t BH = B * H;
+  const int64_t nc = (T + gdn::C - 1) / gdn::C;
+  int nseg = T > 0 ? gdn::plan_segments(BH, nc, 0) : 1;
+  // as many segments as the array holds (fewer segments: a longer chain)
+  while (nseg > 1 && gdn::ws_bytes_for(BH, nseg) > gdn::kScratchBytes) --nseg;
+  if (nseg == 2) nseg = 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (nseg == 1)  // no scratch: nothing to order
+    return gdn::run(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                    static_cast<const bf16*>(v), g, beta, h0, static_cast<bf16*>(o), hT, (int)B,
+                    (int)T, (int)H, scale, nullptr, 1, s);
+  gdn::DeviceScratch* d = nullptr;
+  if (int e = gdn::scratch_of(&d)) return e;
+  // Calls that use the array run one after the other on the device: each
+  // waits for the previous one's completion event (recorded on whatever
+  // stream that call ran on) and records its own.  Under stream capture the
+  // graph's own order applies and the event is left alone.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t he = hipStreamIsCapturing(s, &cap);
+  if (he != hipSuccess) return (int)he;
+  const bool order = cap == hipStreamCaptureStatusNone;
+  if (order && d->recorded) {
+    he = hipStreamWaitEvent(s, d->last, 0);
+    if (he != hipSuccess) return (int)he;
+  }
+  const int e = gdn::run(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                         static_cast<const bf16*>(v), g, beta, h0, static_cast<bf16*>(o), hT,
+                         (int)B, (int)T, (int)H, scale, d->ptr, nseg, s);
+  if (e) return e;
+  if (order) {
+    he = hipEventRecord(d->last, s);
+    if (he != hipSuccess) return (int)he;
+    d->recorded = true;
+  }
+  return 0;
 }

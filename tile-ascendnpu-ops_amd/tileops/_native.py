@@ -77,6 +77,18 @@ SIGNATURES = {
         ctypes.c_size_t,
         [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64],
     ),
+    "tileops_gdn_prefill_fwd_ex": (
+        _c_int,
+        [
+            _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+            _c_float, _c_int, _c_i64, _c_p, ctypes.c_size_t, _c_p,
+        ],
+    ),
+    "tileops_gdn_prefill_workspace_bytes_ex": (
+        ctypes.c_size_t,
+        [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64],
+    ),
     "tileops_gdn_prefill_fwd_noalloc": (
         _c_int,
         [

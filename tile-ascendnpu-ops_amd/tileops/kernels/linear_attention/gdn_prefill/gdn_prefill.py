@@ -6,9 +6,12 @@ recurrence follows golden_gdn_sequential
 form of examples/gdn_prefill/DESIGN.md:6-17.  Layout is ``[B, T, H, D]``
 (token-major, as ``chunk_gated_delta_rule`` takes it): q, k: ``[B, T, H, K]``
 bf16, v: ``[B, T, H, V]`` bf16, g (log-decay) and beta: ``[B, T, H]`` fp32,
-initial / final state ``[B, H, K, V]`` fp32.  Two launches: a parallel
-per-chunk preparation into a workspace, then the sequential recurrence.
-Device code: gdn_prep_kernel, gdn_recur_kernel in csrc/gdn.hip.
+initial / final state ``[B, H, K, V]`` fp32.  The sequence runs in
+segments (config ``segments``: 0 lets the library choose from the head
+count and the device's compute units): one launch runs segment 0 exactly
+and the state maps of the inner segments, a second composes each later
+segment's start state and runs it exactly.  The workspace holds the maps
+(64 KiB per map and head).  Device code: gdn_fused_kernel in csrc/gdn.hip.
 """
 
 from typing import Optional, Tuple
@@ -34,7 +37,8 @@ class GDNPrefillFwdKernel(Kernel):
     """
 
     SUPPORTED_DTYPES = (torch.bfloat16,)
-    profile_kernel_name = r"gdn(?:::|\d+)gdn_(prep|recur)_kernel"
+    tunable_config = ("segments",)
+    profile_kernel_name = r"gdn(?:::|\d+)gdn_(fused|copy_state)_kernel"
 
     def __init__(
         self,
@@ -71,13 +75,14 @@ class GDNPrefillFwdKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # value columns per recurrence workgroup (compiled in)
-        return {"chunk_size": self.chunk_size, "value_slice": 32}
+        # sequence segments run in parallel (0: the library's choice)
+        return {"chunk_size": self.chunk_size, "segments": 0}
 
     def workspace_bytes(self) -> int:
         return int(
-            _native.lib().tileops_gdn_prefill_workspace_bytes(
-                self.batch, self.seq_len, self.heads, self.dim_k, self.dim_v, self.chunk_size
+            _native.lib().tileops_gdn_prefill_workspace_bytes_ex(
+                self.batch, self.seq_len, self.heads, self.dim_k, self.dim_v, self.chunk_size,
+                int(self.config.get("segments", 0)),
             )
         )
 
@@ -118,13 +123,13 @@ class GDNPrefillFwdKernel(Kernel):
         need = self.workspace_bytes()
         if workspace is None or workspace.numel() < need:
             workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
-        code = _native.lib().tileops_gdn_prefill_fwd(
+        code = _native.lib().tileops_gdn_prefill_fwd_ex(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
             initial_state.data_ptr() if initial_state is not None else None,
             o.data_ptr(), final_state.data_ptr(),
             B, T, H, self.dim_k, self.dim_v, self.chunk_size, float(self.scale),
-            _native.dtype_code(self.dtype), workspace.data_ptr(), workspace.numel(),
-            _native.stream_of(q),
+            _native.dtype_code(self.dtype), int(self.config.get("segments", 0)),
+            workspace.data_ptr(), workspace.numel(), _native.stream_of(q),
         )
-        _native.check(code, "tileops_gdn_prefill_fwd")
+        _native.check(code, "tileops_gdn_prefill_fwd_ex")
         return o, final_state
