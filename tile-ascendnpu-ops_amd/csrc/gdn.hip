@@ -23,11 +23,14 @@
 // nc chunks are cut into N segments:
 //   launch 1: segment 0 runs exactly from h0 (outputs, end state), segments
 //             1 .. N-2 run from [0 | I] over 256 columns (Bseg | Phi);
-//   launch 2: segment j >= 1 composes its start state from segment 0's end
-//             state through the maps of segments 1 .. j-1, then runs
-//             exactly (outputs; the last segment writes hT).
-// The composition uses split-bf16 products (hi*hi + hi*lo + lo*hi).  With
-// N = 1 a single launch runs every chunk from h0.
+//   between:  a small launch composes the start states of segments
+//             2 .. N-1 from segment 0's end state through the maps;
+//   launch 2: segments 1 .. N-1 run exactly from their start states
+//             (outputs; the last segment writes hT).
+// The composition uses split-bf16 products (hi*hi + hi*lo + lo*hi): launch 1
+// stores each Phi already split, as a bf16 hi image and a bf16 lo image, so
+// the composition loads them straight into LDS.  With N = 1 a single launch
+// runs every chunk from h0.
 //
 // Workgroup (one per (head, segment)): NCW chain wavefronts and 4 prep
 // wavefronts (launch 1: NCW = 8, three wavefronts per SIMD; launch 2 and
@@ -47,7 +50,7 @@
 //              scan two chunks ahead, and the direct-to-LDS loads of the
 //              chunk operands (the chain wavefronts form Aqk, and L21 when
 //              there are four of them).
-// Three workgroup barriers per chunk.  Every chunk operand crosses HBM once
+// Two workgroup barriers per chunk.  Every chunk operand crosses HBM once
 // per pass over its segment, and nothing per chunk is written back.
 #include <algorithm>
 #include <mutex>
@@ -483,35 +486,25 @@ __device__ __forceinline__ void split8(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo)
   lo = pack8(ra, rb);
 }
 
-// s <- Phi s + Bseg for this wavefront's columns (Bseg K x DV and Phi K x K,
-// fp32 row-major), one column block at a time.
+// A map's Phi stored already split: the [128][128] bf16 image of hi, then
+// that of lo (the values split8 forms from the fp32 entries).
 template <int NB>
-__device__ __forceinline__ void state_compose(f32x4 (&s)[NB][8], const float* phi,
-                                              const float* bseg, int col0, int g, int ln) {
+__device__ __forceinline__ void phi_store(const f32x4 (&s)[NB][8], float* slot, int col0, int g,
+                                          int ln) {
+  bf16* hi = reinterpret_cast<bf16*>(slot);
+  bf16* lo = hi + DK * DV;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    bf16x8 bh[4], bl[4];
+  for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) split8(s[nb][2 * ks], s[nb][2 * ks + 1], bh[ks], bl[ks]);
+    for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
-      f32x4 acc;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = bseg[acc_row(kb, g, r) * DV + col0 + 16 * nb + ln];
-      const float* prow = phi + lam(kb, ln) * DK + 8 * g;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const float4 x0 = *reinterpret_cast<const float4*>(prow + 32 * ks);
-        const float4 x1 = *reinterpret_cast<const float4*>(prow + 32 * ks + 4);
-        bf16x8 ah, al;
-        split8(f32x4{x0.x, x0.y, x0.z, x0.w}, f32x4{x1.x, x1.y, x1.z, x1.w}, ah, al);
-        acc = mfma16(ah, bh[ks], acc);
-        acc = mfma16(ah, bl[ks], acc);
-        acc = mfma16(al, bh[ks], acc);
+      for (int r = 0; r < 4; ++r) {
+        const float x = s[nb][kb][r];
+        const bf16 xh = (bf16)x;
+        const int idx = acc_row(kb, g, r) * DV + col0 + 16 * nb + ln;
+        hi[idx] = xh;
+        lo[idx] = (bf16)(x - (float)xh);
       }
-      s[nb][kb] = acc;
-    }
-  }
 }
 
 // k^T as the A operand of S' for key block kb and token step ts: lane-row m
@@ -792,14 +785,13 @@ __device__ void run_chain(const Args& A, Smem& sm, const Seg& sg, int wave, bool
   ChainTmp<NB> tmp;
   if (!idle) {
     if (OUT) {
-      if (sg.seg == 0) {
-        state_load<NB>(s, A.h0 ? A.h0 + (size_t)sg.bh * kStateFloats : nullptr, col0, g, ln);
-      } else {
-        state_load<NB>(s, ws_slot(A, sg.bh, 0), col0, g, ln);
-        for (int j = 1; j < sg.seg; ++j)
-          state_compose<NB>(s, ws_slot(A, sg.bh, 1 + 2 * (j - 1)),
-                            ws_slot(A, sg.bh, 2 + 2 * (j - 1)), col0, g, ln);
-      }
+      // segment 0 starts from h0, segment 1 from segment 0's end state, a
+      // later segment j from the state gdn_compose_kernel left in the slot of
+      // Bseg_{j-1}
+      const float* src = sg.seg == 0 ? (A.h0 ? A.h0 + (size_t)sg.bh * kStateFloats : nullptr)
+                         : sg.seg == 1 ? ws_slot(A, sg.bh, 0)
+                                       : ws_slot(A, sg.bh, 2 + 2 * (sg.seg - 2));
+      state_load<NB>(s, src, col0, g, ln);
     } else if (usev) {
       state_load<NB>(s, nullptr, col0, g, ln);
     } else {
@@ -855,8 +847,11 @@ __device__ void run_chain(const Args& A, Smem& sm, const Seg& sg, int wave, bool
       dst = ws_slot(A, sg.bh, 0);  // segment 0's end state for the composition
     else
       return;  // an inner exact segment: its end state is not needed
+  } else if (usev) {
+    dst = ws_slot(A, sg.bh, 2 + 2 * (sg.seg - 1));
   } else {
-    dst = ws_slot(A, sg.bh, (usev ? 2 : 1) + 2 * (sg.seg - 1));
+    phi_store<NB>(s, ws_slot(A, sg.bh, 1 + 2 * (sg.seg - 1)), col0, g, ln);
+    return;
   }
   state_store<NB>(s, dst, col0, g, ln);
 }
@@ -988,6 +983,103 @@ __global__ __launch_bounds__(64 * (NCW + 4)) void gdn_fused_kernel(Args A) {
   }
 }
 
+// Start states of the exact segments 2 .. N-1 (between the two launches):
+// S_start(j + 1) = Phi_j S_start(j) + Bseg_j from S_start(1) = segment 0's end
+// state, one workgroup per head: wavefront w keeps columns 16 w .. of the
+// state in registers, the workgroup loads each Phi_j (as its hi and lo bf16
+// images) into LDS by direct-to-LDS loads while the product with the
+// previous one runs, and each composition is written over the columns of
+// Bseg_j it read.  LDS holds an image row r as 16 granules of 16 bytes,
+// granule p at position p ^ phi_swz(r): the 16 rows one operand read
+// touches then fall in distinct bank groups.
+__device__ __forceinline__ int phi_swz(int r) { return (r & 3) | (((r >> 3) & 3) << 2); }
+
+__global__ __launch_bounds__(512) void gdn_compose_kernel(Args A) {
+  __shared__ __attribute__((aligned(16))) bf16 phi_s[2][2 * DK * DK];  // [buf][hi | lo]
+  const int bh = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, g = lane >> 4, ln = lane & 15;
+  const int col0 = 16 * wave;
+  const int nseg = A.nseg;
+  float* const ws_head = A.ws + (size_t)bh * (2 * nseg - 3) * kStateFloats;
+  auto slot = [&](int idx) { return ws_head + (size_t)idx * kStateFloats; };
+  // Phi_j into image buf: 64 windows of 1 KB (four rows each; 0-31 hi,
+  // 32-63 lo), wavefront w issuing windows w, w + 8, ..
+  auto fetch = [&](int j, int buf) {
+    const float* src = slot(1 + 2 * (j - 1));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int win = 8 * i + wave;
+      const int r = 4 * (win & 31) + (lane >> 4);
+      const int p = (lane & 15) ^ phi_swz(r);
+      const uint32_t off = (uint32_t)((win >> 5) * DK * DK * 2 + r * DK * 2 + p * 16);
+      lds_dma16(src, off, lds_addr(&phi_s[buf][win * 512]));
+    }
+  };
+  // B_j of the next pass is loaded into registers a pass ahead, and the
+  // result of a pass is stored during the next one, so that no global
+  // latency sits between two passes
+  auto load_b = [&](f32x4 (&dst)[8], int j) {
+    const float* src = slot(2 + 2 * (j - 1));
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[kb][r] = src[acc_row(kb, g, r) * DV + col0 + ln];
+  };
+  auto store_s = [&](const f32x4 (&src)[8], int j) {
+    float* dst = slot(2 + 2 * (j - 1));
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[acc_row(kb, g, r) * DV + col0 + ln] = src[kb][r];
+  };
+  const int last = nseg - 2;  // maps Phi_1 .. Phi_last
+  f32x4 s[8], bn[8];
+#pragma unroll
+  for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[kb][r] = slot(0)[acc_row(kb, g, r) * DV + col0 + ln];
+  fetch(1, 0);
+  load_b(bn, 1);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  for (int j = 1; j <= last; ++j) {
+    f32x4 acc[8];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) acc[kb] = bn[kb];
+    if (j + 1 <= last) {
+      fetch(j + 1, j & 1);
+      load_b(bn, j + 1);
+    }
+    if (j > 1) store_s(s, j - 1);
+    const bf16* phi_hi = phi_s[(j - 1) & 1];
+    const bf16* phi_lo = phi_hi + DK * DK;
+    bf16x8 bh8[4], bl8[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) split8(s[2 * ks], s[2 * ks + 1], bh8[ks], bl8[ks]);
+    // key step outer, key block inner: the eight accumulators' chains
+    // interleave
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        const int row = lam(kb, ln);
+        const int at = row * DK + 8 * ((4 * ks + g) ^ phi_swz(row));
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(phi_hi + at);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(phi_lo + at);
+        acc[kb] = mfma16(ah, bh8[ks], acc[kb]);
+        acc[kb] = mfma16(ah, bl8[ks], acc[kb]);
+        acc[kb] = mfma16(al, bh8[ks], acc[kb]);
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) s[kb] = acc[kb];
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next Phi and B have landed
+    __syncthreads();
+  }
+  store_s(s, last);
+}
+
 // State pass-through for T = 0: hT = h0 (or 0).
 __global__ __launch_bounds__(256) void gdn_copy_state_kernel(const float* h0, float* hT,
                                                              int64_t n) {
@@ -1071,6 +1163,10 @@ static int run(const bf16* q, const bf16* k, const bf16* v, const float* g, cons
   a.phase = 1;
   gdn_fused_kernel<8><<<dim3(grid), dim3(64 * 12), 0, s>>>(a);
   if (int e = launch_status()) return e;
+  if (nseg > 2) {
+    gdn_compose_kernel<<<dim3((unsigned)BH), dim3(512), 0, s>>>(a);
+    if (int e = launch_status()) return e;
+  }
   a.phase = 2;
   gdn_fused_kernel<4><<<dim3(grid), dim3(64 * 8), 0, s>>>(a);
   return launch_status();

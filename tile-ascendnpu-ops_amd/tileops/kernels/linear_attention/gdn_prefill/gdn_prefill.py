@@ -38,7 +38,7 @@ class GDNPrefillFwdKernel(Kernel):
 
     SUPPORTED_DTYPES = (torch.bfloat16,)
     tunable_config = ("segments",)
-    profile_kernel_name = r"gdn(?:::|\d+)gdn_(fused|copy_state)_kernel"
+    profile_kernel_name = r"gdn(?:::|\d+)gdn_(fused|compose|copy_state)_kernel"
 
     def __init__(
         self,
