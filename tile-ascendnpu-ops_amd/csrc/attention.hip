@@ -70,8 +70,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // cover all 64 banks once.
 template <int D> struct Swz {
   static constexpr int CPR = D / 8;  // chunks per row
-  __device__ __forceinline__ static int k_key(int r) { return CPR >= 16 ? (r & 15) : ((r >> 1) & 7); }
-  __device__ __forceinline__ static int v_key(int r) { return CPR == 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+  __host__ __device__ static constexpr int k_key(int r) { return CPR >= 16 ? (r & 15) : ((r >> 1) & 7); }
+  __host__ __device__ static constexpr int v_key(int r) { return CPR == 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 };
 
 // Workgroup barrier that waits only for this wavefront's LDS accesses, so
@@ -173,8 +173,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // the register loads)
   constexpr bool QLDS = NSLOT == 2 && !CAUSAL;
 
-  __shared__ __attribute__((aligned(16))) T k_lds[NSLOT * TILE_K];
-  __shared__ __attribute__((aligned(16))) T v_lds[NSLOT * TILE_V];
+  // (aligned so that the XOR-formed operand addresses below hold)
+  __shared__ __attribute__((aligned(1024))) T k_lds[NSLOT * TILE_K];
+  __shared__ __attribute__((aligned(1024))) T v_lds[NSLOT * TILE_V];
   // group A's query rows during the prologue (with QLDS)
   __shared__ __attribute__((aligned(16))) T q_lds[QLDS ? 128 * D : 8];
 
@@ -249,6 +250,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
 
+  // last visible key of this lane's query row, less the lane half's key
+  // offset inside a 32-key block (4 half): the masks below compare the
+  // block-relative key index against it
+  const int mask_lim = (CAUSAL ? min(Skv - 1, qi + off) : Skv - 1) - 4 * half;
   const int kv_end = CAUSAL ? min(Skv, q0 + BM + off) : Skv;
   const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
@@ -311,43 +316,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float l_run = 0.0f;
   const float lazy_raw = kLazyLog2 / scale_log2;
 
-  // Lane-dependent element offsets of the operand reads (the slot base is
-  // added per read).
-  // K (S^T A operand): row kb * 32 + col, chunk 2 ks + half, swizzled; the kb
-  // term is a constant added at the read.
-  int koff[KSTEPS];
-#pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks)
-    koff[ks] = col * D + (((ks * 2 + half) ^ Swz<D>::k_key(col)) << 3);
+  // Lane-dependent LDS byte addresses of the operand reads, one register per
+  // operand: the per-step terms enter by XOR, the slot and key-block terms
+  // as DS immediate offsets.
+  // K (S^T A operand): row kb * 32 + col, chunk (2 ks + half) ^ key(col).
+  // As 2 ks + half = 2 ks ^ half, the byte offset col 2D + 16 ((2 ks + half)
+  // ^ key) equals (col 2D + 16 (half ^ key)) ^ 32 ks: the bits of 32 ks
+  // (5 .. log2(2D) - 1) are clear in col 2D and in the LDS base (aligned).
+  const uint32_t kbx = lds_addr(k_lds) + (uint32_t)(col * D * (int)sizeof(T)) +
+                       16u * (uint32_t)(half ^ Swz<D>::k_key(col));
   // V^T (O^T A operand) through transpose reads: in each group of 16 lanes,
   // lane j points at 4 dims (4 (j % 4) ..) of key row j / 4 and receives
   // dim j of those 4 keys.  Key slot 4 rr + e of lane half g is key
   // 16 ks + 8 rr + 4 g + e, the order in which P^T sits in registers; the
   // ks and rr terms are constants (the swizzle key depends on row % 4 only).
+  // Dim block db adds 4 db to the chunk index, and the swizzle key is a
+  // multiple of 4 below 4 DBLK, so the block enters as XOR with 64 db.
   const int grp16 = lane >> 4, j16 = lane & 15;
   const int vrow = 4 * (grp16 >> 1) + (j16 >> 2);
-  int voff[DBLK];
-#pragma unroll
-  for (int db = 0; db < DBLK; ++db) {
-    const int dim = db * 32 + 16 * (grp16 & 1) + 4 * (j16 & 3);
-    voff[db] = vrow * DV + ((((dim >> 3) ^ Swz<DV>::v_key(vrow)) << 3) | (dim & 7));
+  uint32_t vbx;
+  {
+    const int dim = 16 * (grp16 & 1) + 4 * (j16 & 3);
+    vbx = lds_addr(v_lds) +
+          (uint32_t)((vrow * DV + ((((dim >> 3) ^ Swz<DV>::v_key(vrow)) << 3) | (dim & 7))) *
+                     (int)sizeof(T));
   }
-
-  // Operand reads: `vb0` / `kb0` are the LDS byte addresses of this lane's
-  // first V^T / K element in slot 0, made opaque once, so that the
-  // per-read constants (slot, key and head-dim steps) become DS immediate
-  // offsets rather than one address computation per read.
-  uint32_t vb0[DBLK], kb0[KSTEPS];
-#pragma unroll
-  for (int db = 0; db < DBLK; ++db) {
-    vb0[db] = lds_addr(v_lds) + voff[db] * (uint32_t)sizeof(T);
-    asm volatile("" : "+v"(vb0[db]));
-  }
-#pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks) {
-    kb0[ks] = lds_addr(k_lds) + koff[ks] * (uint32_t)sizeof(T);
-    asm volatile("" : "+v"(kb0[ks]));
-  }
+  static_assert(Swz<DV>::v_key(0) == 0 && Swz<DV>::v_key(3) % 4 == 0, "V swizzle key");
   typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
   typedef __attribute__((address_space(3))) V8 lds_v8;
   // A operand of the O^T update: 8 keys (16 ks + 8 rr + ..) of dim block db,
@@ -389,18 +383,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int kb = 0; kb < NKB; ++kb) acc_s[kb] = f32x16{};
     }
     // slot offsets: immediate DS offsets when the slot is a compile-time
-    // constant (the unrolled loop), one add per address otherwise
-    uint32_t vb[DBLK], kb[KSTEPS];
+    // constant (the unrolled loop), one add per address otherwise.  The
+    // base registers pass through an empty asm here, so that the per-step
+    // XORs are formed inside the phase rather than hoisted into one
+    // register each for the whole kernel.
+    uint32_t kx = kbx, vx = vbx;
+    asm volatile("" : "+v"(kx), "+v"(vx));
     const uint32_t vso = (uint32_t)(int)vslot * TILE_V * (uint32_t)sizeof(T);
     const uint32_t kso = (uint32_t)(int)kslot * TILE_K * (uint32_t)sizeof(T);
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db) vb[db] = vb0[db] + vso;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) kb[ks] = kb0[ks] + kso;
+    auto vb = [&](int db) __device__ __attribute__((always_inline)) {
+      return (vx ^ (64u * (uint32_t)db)) + vso;
+    };
+    auto kb = [&](int ks) __device__ __attribute__((always_inline)) {
+      return (kx ^ (32u * (uint32_t)ks)) + kso;
+    };
     auto fetch = [&](int n) __device__ __attribute__((always_inline)) -> V8 {
       const int j = n / W, w = n % W;
-      if (w < WO) return read_vt(vb[w], j);
-      return read_k(kb[KS4 * j + (w - WO) / NKB], (w - WO) % NKB);
+      if (w < WO) return read_vt(vb(w), j);
+      return read_k(kb(KS4 * j + (w - WO) / NKB), (w - WO) % NKB);
     };
     // LDS read instructions of operand n: two transpose reads for V^T, one
     // 16-byte read for K (the scheduling-group sizes must be constants)
@@ -469,13 +469,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // masking only on the ragged last tile and on causal diagonal tiles
     // (a workgroup-uniform branch, kept out of the common path)
     if ((kv0 + BN > Skv) || (CAUSAL && kv0 + BN - 1 > q0 + off)) {
-      const int lim = CAUSAL ? min(Skv - 1, qi + off) : Skv - 1;  // last visible key
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int kv = kv0 + kb * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-          acc_s[kb][r] = kv > lim ? -INFINITY : acc_s[kb][r];
+          const int kv = kv0 + kb * 32 + (r >> 2) * 8 + (r & 3);  // key less 4 half
+          acc_s[kb][r] = kv > mask_lim ? -INFINITY : acc_s[kb][r];
         }
       }
     }
@@ -549,7 +548,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     {
       const uint32_t qb = lds_addr(grp_a ? q_lds : v_lds + TILE_V) + (uint32_t)gw * 32 * D * 2;
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) qreg[ks] = read_k(kb0[ks] - lds_addr(k_lds) + qb, 0);
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        qreg[ks] = read_k((kbx ^ (32u * (uint32_t)ks)) - lds_addr(k_lds) + qb, 0);
     }
   } else {
     // K(0), K(1) (group B) and V(0) (group A) into their slots
