@@ -128,7 +128,7 @@ class _ReduceOpBase(Op):
             )
         dim = self.dim % x.ndim
         N = x.shape[dim]
-        M = prod(s for i, s in enumerate(x.shape) if i != dim)
+        M = prod([s for i, s in enumerate(x.shape) if i != dim])
         self._last_roofline_mn = (M, N)
         if dim != x.ndim - 1:
             x = x.movedim(dim, -1)

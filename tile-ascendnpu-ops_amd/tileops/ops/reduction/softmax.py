@@ -91,7 +91,7 @@ class LogSumExpFwdOp(Op):
         dim = self.dim
         if isinstance(dim, (list, tuple)) or dim is None:
             dims = normalize_dim(dim, x.ndim, empty_dim_policy=self._empty_dim_policy)
-            self._static_axes = frozenset((0, d) for d in dims)
+            self._static_axes = frozenset([(0, d) for d in dims])
             x, orig_shape, _ = flatten_for_multidim(x, dims)
             N = x.shape[-1]
             M = prod(x.shape[:-1])
@@ -114,7 +114,7 @@ class LogSumExpFwdOp(Op):
                 f"x.shape[{dim}]={N}"
             )
         self._static_axes = frozenset({(0, d)})
-        M = prod(s for i, s in enumerate(x.shape) if i != d)
+        M = prod([s for i, s in enumerate(x.shape) if i != d])
         self._last_roofline_spec = (M, N, x.dtype)
         moved = d != x.ndim - 1
         if moved:
