@@ -190,7 +190,7 @@ int tileops_argreduce_fwd(const void* x, int64_t* y, int64_t M, int64_t N, int d
  *   o:    [B, Sq,  H,   D]    lse:  [B, H, Sq] float32 (log2 domain:
  *                               logsumexp(scale * q k^T, masked) / ln 2)
  * Causal masking is right-aligned: query i sees keys j <= i + (Skv - Sq).
- * H % Hkv == 0 (grouped-query sharing); D must be 64, 128 or 256.
+ * H % Hkv == 0 (grouped-query sharing); D must be 64, 96, 128, 192 or 256.
  * softcap > 0 caps the scores, softcap * tanh(scale q.k / softcap), before
  * the mask and the softmax (the lse is then of the capped scores); 0 turns
  * it off; negative, NaN or infinite values are TILEOPS_EINVAL.

@@ -144,6 +144,38 @@ def test_mha_head_dim_256(causal, dtype, B, H, Hkv, sq, skv):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D, dtype, B, H, Hkv, sq, skv", [
+    (96, torch.bfloat16, 2, 4, 4, 512, 512),
+    (96, torch.float16, 1, 4, 2, 300, 437),    # grouped heads, ragged, right-aligned causal
+    (96, torch.bfloat16, 1, 2, 1, 64, 1100),   # one query block, many key tiles
+    (192, torch.bfloat16, 2, 4, 4, 512, 512),
+    (192, torch.float16, 1, 4, 2, 300, 437),
+    (192, torch.bfloat16, 1, 2, 1, 64, 1100),
+])
+def test_mha_head_dims_96_192(causal, D, dtype, B, H, Hkv, sq, skv):
+    # head dims that are multiples of 32 but not powers of two (the
+    # reference's tile sizing, multi_head_attention.py:251, admits any dim):
+    # the LDS rows are padded to 128 / 256 elements; 192 runs as two
+    # workgroups per query block with 96 output columns each
+    q = torch.randn(B, sq, H, D, device="cuda", dtype=dtype)
+    k = torch.randn(B, skv, Hkv, D, device="cuda", dtype=dtype)
+    v = torch.randn(B, skv, Hkv, D, device="cuda", dtype=dtype)
+    o, lse = GQAPrefillFwdKernel(B, H, Hkv, sq, skv, D, causal, dtype)(q, k, v)
+    assert o.shape == q.shape and lse.shape == (B, H, sq)
+    _check(q, k, v, o, lse, causal)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_op_head_dim_96(causal):
+    B, S, H, D = 1, 700, 4, 96
+    q, k, v = MhaFwdWorkload(B, H, S, D, causal, torch.bfloat16).gen_inputs()
+    o, lse = MultiHeadAttentionFwdOp(B, H, S, D, causal, torch.bfloat16)(q, k, v)
+    _check(q, k, v, o, lse, causal)
+
+
+@pytest.mark.gpu
 def test_mha_peaked_attention():
     # one key per query dominates: exercises large score ranges and rescaling
     B, S, H, D = 1, 256, 2, 64

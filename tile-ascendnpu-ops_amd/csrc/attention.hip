@@ -25,6 +25,11 @@
 //
 // The softmax runs in the log2 domain (scores scaled by scale * log2 e); the
 // per-row LSE written out is m + log2(l), i.e. logsumexp(scale q k^T) / ln 2.
+//
+// Head dims that are not powers of two (96, 192) keep the LDS images of the
+// next power of two (rows of 128 or 256 elements, the same swizzles): the
+// padding chunks are filled with a copy of a real chunk of the row and never
+// read, and the MFMA steps cover the real dims only.
 #include <float.h>
 #include <stdlib.h>
 
@@ -149,8 +154,8 @@ __device__ __forceinline__ float tanh_sat(float y) {
 // units from the start of the softmax: the caller passes scale_log2 = 1,
 // cap_scale = scale / softcap and cap_log2 = softcap * log2 e.
 // D: the head dim of q, k and v rows; DV: the v columns (and output columns)
-// a workgroup computes, D itself up to 128, half of it for D = 256 (two
-// workgroups per query block, each forming the full scores).
+// a workgroup computes, D itself up to 128, half of it for D = 192 and 256
+// (two workgroups per query block, each forming the full scores).
 template <typename T, int D, int DV, bool CAUSAL, int BN, bool SOFTCAP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void mha_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
@@ -161,17 +166,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int BM = 256;         // query rows per workgroup (8 x 32)
   constexpr int KSTEPS = D / 16;  // MFMA steps over the head dim
   constexpr int DBLK = DV / 32;   // 32-row blocks of O^T
-  constexpr int TILE_K = BN * D;  // elements per K tile
-  constexpr int TILE_V = BN * DV; // elements per V tile (this workgroup's columns)
+  // LDS row widths: the next power of two of D and DV
+  constexpr int DP = D <= 64 ? 64 : D <= 128 ? 128 : 256;
+  constexpr int DVP = DV <= 64 ? 64 : 128;
+  constexpr int TILE_K = BN * DP;  // elements per K tile
+  constexpr int TILE_V = BN * DVP; // elements per V tile (this workgroup's columns)
   constexpr int NW_K = TILE_K / 2048, NW_V = TILE_V / 2048;  // 1 KB windows per wavefront
-  static_assert(BN == 64 || (BN == 128 && D == 128), "tile shapes");
-  static_assert(DV == D || (D == 256 && DV == 128), "value split");
+  static_assert(D % 32 == 0 && DV % 32 == 0 && DV <= 128, "head dims");
+  static_assert(BN == 64 || (BN == 128 && DP == 128), "tile shapes");
+  static_assert(DV == D || (D == 2 * DV && D >= 192), "value split");
   static_assert(NW_V >= 1 && NW_K <= 15, "vmcnt immediate");
   constexpr int NSLOT = BN == 64 ? 3 : 2;  // LDS slots per operand
   // Q through LDS in the prologue (non-causal 128-key tiles; measured
   // 1.5 % faster there and 1.5 % slower on the causal blocks, which keep
   // the register loads)
-  constexpr bool QLDS = NSLOT == 2 && !CAUSAL;
+  constexpr bool QLDS = NSLOT == 2 && !CAUSAL && D == DP;
 
   // (aligned so that the XOR-formed operand addresses below hold)
   __shared__ __attribute__((aligned(1024))) T k_lds[NSLOT * TILE_K];
@@ -193,7 +202,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // differ in length: they go longest first over pairs of heads (the query
   // blocks of two heads interleaved), so that the last workgroups an XCD
   // receives are short ones.
-  // (the value halves of one query block, D = 256, are neighbours)
+  // (the value halves of one query block, D = 192 and 256, are neighbours)
   constexpr int NDV = D / DV;
   const int nblk = (int)gridDim.x;
   int id = blockIdx.x;
@@ -264,7 +273,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // min(r, rmax): rows past the last key repeat it (their scores are
   // masked).  When WROWS is a multiple of the swizzle key's period (16 rows)
   // the key depends only on rl and the chunk's byte offset is one per-lane
-  // constant; with 512-byte rows (D = 256, WROWS = 8) it is formed per
+  // constant; with 512-byte rows (D = 192 and 256, WROWS = 8) it is formed per
   // window.  A tile past the last one
   // (the schedule issues its loads regardless) re-reads the last tile into
   // its own slot, which no phase reads, so every load is in bounds and the
@@ -272,11 +281,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint32_t row_bytes = (uint32_t)(kv_row * sizeof(T));
   auto loader = [&](auto is_v) __device__ __attribute__((always_inline)) {
     constexpr bool IS_V = decltype(is_v)::value;
-    constexpr int DL = IS_V ? DV : D, CPR = DL / 8, WROWS = 256 / CPR;
+    constexpr int DL = IS_V ? DVP : DP, CPR = DL / 8, WROWS = 256 / CPR;
+    constexpr int RCPR = (IS_V ? DV : D) / 8;  // chunks of a row in global memory
     constexpr int TL = BN * DL;
     const int rl = gw * (64 / CPR) + lane / CPR;
     auto key = [](int r) { return IS_V ? Swz<DL>::v_key(r) : Swz<DL>::k_key(r); };
-    const uint32_t cbyte = (uint32_t)((((lane % CPR) ^ key(rl)) << 3) * sizeof(T));
+    // global chunk of LDS position p of row r; a padding position takes a
+    // copy of real chunk c - (CPR - RCPR), never read
+    auto gchunk = [](int p, int r) {
+      const int c = p ^ (IS_V ? Swz<DL>::v_key(r) : Swz<DL>::k_key(r));
+      return c < RCPR ? c : c - (CPR - RCPR);
+    };
+    (void)key;
+    const uint32_t cbyte = (uint32_t)((gchunk(lane % CPR, rl) << 3) * sizeof(T));
     const T* gsrc = IS_V ? vbase : kbase;
     T* gdst = IS_V ? v_lds : k_lds;
     return [=](int t, int i) __device__ __attribute__((always_inline)) {
@@ -286,7 +303,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const uint32_t lds = lds_addr(gdst + (uint32_t)(t % NSLOT) * TL) + (uint32_t)gw * 1024;
       const int r = i * WROWS + rl;
       const uint32_t cb =
-          WROWS % 16 == 0 ? cbyte : (uint32_t)((((lane % CPR) ^ key(r)) << 3) * sizeof(T));
+          WROWS % 16 == 0 ? cbyte : (uint32_t)((gchunk(lane % CPR, r) << 3) * sizeof(T));
       lds_dma16(src, (uint32_t)min(r, rmax) * row_bytes + cb, lds + i * 4096);
     };
   };
@@ -323,8 +340,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // As 2 ks + half = 2 ks ^ half, the byte offset col 2D + 16 ((2 ks + half)
   // ^ key) equals (col 2D + 16 (half ^ key)) ^ 32 ks: the bits of 32 ks
   // (5 .. log2(2D) - 1) are clear in col 2D and in the LDS base (aligned).
-  const uint32_t kbx = lds_addr(k_lds) + (uint32_t)(col * D * (int)sizeof(T)) +
-                       16u * (uint32_t)(half ^ Swz<D>::k_key(col));
+  const uint32_t kbx = lds_addr(k_lds) + (uint32_t)(col * DP * (int)sizeof(T)) +
+                       16u * (uint32_t)(half ^ Swz<DP>::k_key(col));
   // V^T (O^T A operand) through transpose reads: in each group of 16 lanes,
   // lane j points at 4 dims (4 (j % 4) ..) of key row j / 4 and receives
   // dim j of those 4 keys.  Key slot 4 rr + e of lane half g is key
@@ -338,29 +355,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   {
     const int dim = 16 * (grp16 & 1) + 4 * (j16 & 3);
     vbx = lds_addr(v_lds) +
-          (uint32_t)((vrow * DV + ((((dim >> 3) ^ Swz<DV>::v_key(vrow)) << 3) | (dim & 7))) *
+          (uint32_t)((vrow * DVP + ((((dim >> 3) ^ Swz<DVP>::v_key(vrow)) << 3) | (dim & 7))) *
                      (int)sizeof(T));
   }
-  static_assert(Swz<DV>::v_key(0) == 0 && Swz<DV>::v_key(3) % 4 == 0, "V swizzle key");
+  static_assert(Swz<DVP>::v_key(0) == 0 && Swz<DVP>::v_key(3) % 4 == 0, "V swizzle key");
   typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
   typedef __attribute__((address_space(3))) V8 lds_v8;
   // A operand of the O^T update: 8 keys (16 ks + 8 rr + ..) of dim block db,
   // two 64-bit transpose reads assembled by whole-register moves
   auto read_vt = [&](uint32_t vb, int ks) __device__ __attribute__((always_inline)) -> V8 {
-    const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks) * DV * 2));
-    const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks + 8) * DV * 2));
+    const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks) * DVP * 2));
+    const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(uintptr_t)(vb + (16 * ks + 8) * DVP * 2));
     const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
     const u32x4 w = {y0.x, y0.y, y1.x, y1.y};
     return __builtin_bit_cast(V8, w);
   };
   auto read_k = [&](uint32_t kb, int blk) __device__ __attribute__((always_inline)) -> V8 {
-    return *(lds_v8*)(uintptr_t)(kb + blk * 32 * D * 2);
+    return *(lds_v8*)(uintptr_t)(kb + blk * 32 * DP * 2);
   };
 
   // The MFMA phase as one sequence: per 16-key step j, the DBLK O^T blocks
-  // of keys 16 j .. 16 j + 15 (when DO_O), then the S^T products of head-dim
-  // steps KS4 j .. KS4 j + KS4 - 1 for both 32-key blocks (when DO_S), so
-  // that up to DBLK + 2 independent accumulators alternate.  Each operand is
+  // of keys 16 j .. 16 j + 15 (when DO_O), then WS of the KSTEPS x NKB S^T
+  // products (head-dim step major, key block minor: products WS j .. WS j
+  // + WS - 1) (when DO_S), so that up to DBLK + NKB independent accumulators
+  // alternate.  Each operand is
   // read from LDS PF MFMAs ahead into a ring of PF + 1 register sets, and
   // the order MFMA, then the reads of the operand PF ahead, is pinned with
   // scheduling groups: left alone, the scheduler issues most reads just
@@ -372,12 +390,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int LD = decltype(ld)::value;  // 0: no loads, 1: V windows, 2: K windows
     constexpr int NWL = LD == 1 ? NW_V : LD == 2 ? NW_K : 1;
     constexpr int J = BN / 16;                             // 16-key steps per tile
-    constexpr int KS4 = KSTEPS / J;                        // head-dim steps per 16-key step
-    constexpr int WO = DO_O ? DBLK : 0, WS = DO_S ? KS4 * NKB : 0;
+    constexpr int WO = DO_O ? DBLK : 0, WS = DO_S ? KSTEPS * NKB / J : 0;
     constexpr int W = WO + WS;                             // MFMAs per 16-key step
     constexpr int N = J * W;
+    // windows issued at MFMAs LDSTEP i + LDPOS, i < NWL
     constexpr int LDSTEP = N / NWL, LDPOS = LDSTEP > 5 ? 5 : LDSTEP - 1;
-    static_assert(KSTEPS % J == 0, "head-dim steps per 16-key step");
+    static_assert((KSTEPS * NKB) % J == 0, "S products per 16-key step");
     if (DO_S) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) acc_s[kb] = f32x16{};
@@ -400,7 +418,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto fetch = [&](int n) __device__ __attribute__((always_inline)) -> V8 {
       const int j = n / W, w = n % W;
       if (w < WO) return read_vt(vb(w), j);
-      return read_k(kb(KS4 * j + (w - WO) / NKB), (w - WO) % NKB);
+      const int si = WS * j + (w - WO);  // S product: head-dim step si / NKB, key block si % NKB
+      return read_k(kb(si / NKB), si % NKB);
     };
     // LDS read instructions of operand n: two transpose reads for V^T, one
     // 16-byte read for K (the scheduling-group sizes must be constants)
@@ -421,13 +440,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (w < WO) {
         acc_o[w] = Mfma<T>::run(ring[n % (PF + 1)], pb[j], acc_o[w]);
       } else {
-        const int ks = KS4 * j + (w - WO) / NKB, kb = (w - WO) % NKB;
+        const int si = WS * j + (w - WO);
+        const int ks = si / NKB, kb = si % NKB;
         acc_s[kb] = Mfma<T>::run(ring[n % (PF + 1)], qreg[ks], acc_s[kb]);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // this MFMA
       if (n + PF < N) group_reads(n + PF);
-      if (LD == 1 && n % LDSTEP == LDPOS) load_window_v(lt, n / LDSTEP);
-      if (LD == 2 && n % LDSTEP == LDPOS) load_window_k(lt, n / LDSTEP);
+      if (LD == 1 && n % LDSTEP == LDPOS && n / LDSTEP < NWL) load_window_v(lt, n / LDSTEP);
+      if (LD == 2 && n % LDSTEP == LDPOS && n / LDSTEP < NWL) load_window_k(lt, n / LDSTEP);
     }
   };
   typedef std::integral_constant<bool, true> yes;
@@ -717,8 +737,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const float l_tot = pair_sum(l_run);
   const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   {
-    constexpr int OCPR = DV / 8;                       // 16-byte chunks per output row
-    constexpr int OBLK = 32 * DV;                      // elements of one wavefront's block
+    constexpr int OCPR = DVP / 8;                      // 16-byte chunks per staged row
+    constexpr int OBLK = 32 * DVP;                     // elements of one wavefront's block
     static_assert((NSLOT * TILE_K) % OBLK == 0 && NSLOT * (TILE_K + TILE_V) >= 8 * OBLK,
                   "output staging blocks fit the tile slots");
     T* ot = wave * OBLK < NSLOT * TILE_K ? k_lds + wave * OBLK
@@ -730,8 +750,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         T vals[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) vals[e] = (T)(acc_o[db][g * 4 + e] * inv_l);
-        const int ch = (db * 4 + g) ^ Swz<DV>::k_key(col);  // chunk of d = db * 32 + g * 8
-        *reinterpret_cast<uint2*>(ot + col * DV + ch * 8 + half * 4) =
+        const int ch = (db * 4 + g) ^ Swz<DVP>::k_key(col);  // chunk of d = db * 32 + g * 8
+        *reinterpret_cast<uint2*>(ot + col * DVP + ch * 8 + half * 4) =
             *reinterpret_cast<uint2*>(vals);
       }
     }
@@ -741,9 +761,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int i = 0; i < 32 / RPI; ++i) {
       const int r = i * RPI + rr;  // row of the wavefront's block
       const u32x4 val =
-          *reinterpret_cast<const u32x4*>(ot + r * DV + ((cc ^ Swz<DV>::k_key(r)) << 3));
+          *reinterpret_cast<const u32x4*>(ot + r * DVP + ((cc ^ Swz<DVP>::k_key(r)) << 3));
       const int row = q0 + wave * 32 + r;
-      if (row < Sq)
+      if (row < Sq && cc < DV / 8)
         __builtin_nontemporal_store(
             val, reinterpret_cast<u32x4*>(o + ((int64_t)bb * Sq + row) * q_row +
                                           (int64_t)hq * D + dv0 + cc * 8));
@@ -777,10 +797,11 @@ static int launch_w(const void* q, const void* k, const void* v, void* o, float*
                     int Sq, int Skv, int H, int Hkv, bool causal, float scale, float softcap,
                     hipStream_t s) {
   constexpr float kLog2e = 1.4426950408889634f;
-  // D = 128: 128-key tiles, two slots; D = 64: 64-key tiles, three slots;
-  // D = 256: two workgroups per query block, 128 value columns each
-  constexpr int DV = D == 256 ? 128 : D;
-  constexpr int BN = D == 128 ? 128 : 64;
+  // D = 96, 128: 128-key tiles, two slots; D = 64: 64-key tiles, three
+  // slots; D = 192, 256: two workgroups per query block, each with half the
+  // value columns, 64-key tiles
+  constexpr int DV = D >= 192 ? D / 2 : D;
+  constexpr int BN = D == 128 || D == 96 ? 128 : 64;
   if (softcap > 0.0f)
     launch_k<T, D, DV, BN, true>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, 1.0f,
                                  scale / softcap, softcap * kLog2e, s);
@@ -800,6 +821,10 @@ static int dispatch_d(int D, const void* q, const void* k, const void* v, void* 
     return launch_w<T, 64>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
   if (D == 256)
     return launch_w<T, 256>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
+  if (D == 96)
+    return launch_w<T, 96>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
+  if (D == 192)
+    return launch_w<T, 192>(q, k, v, o, lse, B, Sq, Skv, H, Hkv, causal, scale, softcap, s);
   return TILEOPS_ESHAPE;
 }
 
@@ -813,7 +838,7 @@ extern "C" int tileops_mha_fwd(const void* q, const void* k, const void* v, void
                                int64_t D, int causal, float scale, float softcap, int dtype,
                                void* stream) {
   if (B < 0 || Sq < 0 || Skv < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0) return TILEOPS_ESHAPE;
-  if (D != 64 && D != 128 && D != 256) return TILEOPS_ESHAPE;
+  if (D != 64 && D != 96 && D != 128 && D != 192 && D != 256) return TILEOPS_ESHAPE;
   if (B > INT32_MAX || Sq > INT32_MAX || Skv > INT32_MAX || H > 65535) return TILEOPS_ESHAPE;
   if (causal && Sq > Skv) return TILEOPS_ESHAPE;
   if (dtype != TILEOPS_F16 && dtype != TILEOPS_BF16) return TILEOPS_EINVAL;
@@ -823,8 +848,8 @@ extern "C" int tileops_mha_fwd(const void* q, const void* k, const void* v, void
   if (!q || !k || !v || !o || !lse) return TILEOPS_ENULL;
   if (!host_aligned16(q) || !host_aligned16(k) || !host_aligned16(v) || !host_aligned16(o))
     return TILEOPS_EINVAL;
-  // grid: (Sq / 256) query blocks x H x B (x 2 for D = 256), indexed in int
-  if (((Sq + 255) / 256) * H * B * (D == 256 ? 2 : 1) > (int64_t)INT32_MAX) return TILEOPS_ESHAPE;
+  // grid: (Sq / 256) query blocks x H x B (x 2 for D = 192, 256), indexed in int
+  if (((Sq + 255) / 256) * H * B * (D >= 192 ? 2 : 1) > (int64_t)INT32_MAX) return TILEOPS_ESHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TILEOPS_BF16)
     return mha::dispatch_d<bf16>((int)D, q, k, v, o, lse, (int)B, (int)Sq, (int)Skv, (int)H,

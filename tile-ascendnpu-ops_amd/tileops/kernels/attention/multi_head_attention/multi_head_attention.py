@@ -58,7 +58,7 @@ class GQAPrefillFwdKernel(Kernel):
 
     Args:
         batch, heads, heads_kv, seq_len_q, seq_len_kv, dim: problem shape
-            (``dim`` 64 or 128; ``heads % heads_kv == 0``).
+            (``dim`` 64, 96, 128, 192 or 256; ``heads % heads_kv == 0``).
         is_causal: Apply the right-aligned causal mask.
         dtype: float16 or bfloat16.
         sm_scale: Softmax scale (default ``dim ** -0.5``).
@@ -94,8 +94,10 @@ class GQAPrefillFwdKernel(Kernel):
             raise ValueError(
                 f"{self.__class__.__name__} only supports dtypes [{supported}], got {dtype}"
             )
-        if dim not in (64, 128, 256):
-            raise ValueError(f"{self.__class__.__name__} supports dim 64, 128 or 256, got {dim}")
+        if dim not in (64, 96, 128, 192, 256):
+            raise ValueError(
+                f"{self.__class__.__name__} supports dim 64, 96, 128, 192 or 256, got {dim}"
+            )
         if not (0.0 <= softcap < float("inf")):
             raise ValueError(f"{self.__class__.__name__}: softcap must be finite and >= 0 (got {softcap})")
         self.batch = batch
