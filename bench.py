@@ -266,10 +266,14 @@ def cpu_baselines(only=None) -> dict:
         t = _median_s(lambda: tr.gdn_sequential(q, k, v, g, beta, K**-0.5), reps=1)
         C = 64
         flops = (6 * C * C * K + 4 * C * C * K + 6 * C * K * K + C**3 // 3) * (T // C) * B * H
+        full_s = t * (8192 // T)
         out["GatedDeltaNetPrefillFwdOp"] = entry(
             flops / t / 1e12, "TFLOP/s",
-            f"the first {T} of the 8192 tokens of every (batch, head) (the token "
-            "recurrence's work grows linearly in T), counted with the chunked-form flops")
+            f"the first {T} of the 8192 tokens of every (batch, head), {t:.2f} s, counted "
+            "with the chunked-form flops; the token recurrence's work grows linearly in T, "
+            f"so the full T = 8192 is extrapolated (x {8192 // T}) to {full_s:.1f} s, "
+            "not measured")
+        out["GatedDeltaNetPrefillFwdOp"]["full_workload_s_extrapolated"] = round(full_s, 2)
     cores = {"threads": threads, "host_cpus": os.cpu_count(), "cpu": _cpu_model()}
     for v in out.values():
         v.update(cores)

@@ -298,6 +298,34 @@ def test_rocprof_script_rebuilds_op():
     assert "weights_only=True" in src and "range(5)" in src and "range(10)" in src
 
 
+def test_rocprof_script_settles_and_counts_its_calls(capsys):
+    # the child runs warm-up, then untimed batches for the settle time, then
+    # the measured calls, and prints the total that the parent splits the
+    # dispatches by; run here against a stand-in for torch
+    import types
+
+    class Fn:
+        def __init__(self):
+            self.n = 0
+
+        def __call__(self, *a):
+            self.n += 1
+
+    fake_cuda = types.SimpleNamespace(set_device=lambda i: None, synchronize=lambda: None)
+    fake_torch = types.SimpleNamespace(cuda=fake_cuda, Tensor=torch.Tensor, no_grad=torch.no_grad,
+                                       load=lambda path, weights_only: [1.0])
+    src = rp._generate_script(Fn, "/x/inputs.pt", 3, 7, 0, settle_s=0.05)
+    body = "\n".join(line for line in src.splitlines()
+                     if not line.startswith(("import torch", "from ", "fn = ")))
+    fn = Fn()
+    exec(body, {"torch": fake_torch, "fn": fn})  # noqa: S102
+    out = capsys.readouterr().out
+    total = int(out.split("tileops-rocprof: calls ")[1].split()[0])
+    assert total == fn.n and total >= 3 + 3 + 7  # at least one settle batch of warm_up calls
+    assert (total - 7 - 3) % 3 == 0
+    assert "tileops-rocprof: done" in out
+
+
 def test_rocprof_rejects_closures():
     with pytest.raises(TypeError, match="events mode"):
         rp.bench_kernel_rocprof(lambda x: x, (torch.zeros(1),))
