@@ -298,6 +298,32 @@ def test_rocprof_script_rebuilds_op():
     assert "weights_only=True" in src and "range(5)" in src and "range(10)" in src
 
 
+def test_counter_runs_use_fixed_call_counts(monkeypatch):
+    # the counter passes divide their totals by warm_up + launch_count, so
+    # their child program must not settle; exercised with the rocprofv3
+    # runs replaced by stand-ins
+    from tileops.ops.elementwise.clamp_scalar import ClampScalarFwdOp
+
+    scripts = []
+
+    def fake_run(script, counters, work, timeout, env):
+        scripts.append(open(script).read())
+        return "db"
+
+    totals = {"FETCH_SIZE": 4.0 * 8, "WRITE_SIZE": 2.0 * 8, "SQ_VALU_MFMA_BUSY_CYCLES": 0.0,
+              "GRBM_GUI_ACTIVE": 8.0}
+    monkeypatch.setattr(rp, "counter_calibration", lambda timeout=300: (2.0, 1.0))
+    monkeypatch.setattr(rp, "_run_pmc", fake_run)
+    monkeypatch.setattr(rp, "read_counter_totals", lambda db, regex: dict(totals))
+    op = ClampScalarFwdOp(N_total=4096, dtype=torch.bfloat16, min=-1.0, max=None)
+    res = rp.bench_kernel_counters(op, (torch.zeros(4096, dtype=torch.bfloat16),),
+                                   launch_count=3, warm_up=1)
+    assert len(scripts) == len(rp.COUNTER_PASSES)
+    assert all("< 0.0:" in src for src in scripts)  # no settle time
+    assert res["hbm_read_bytes"] == 4 * 8 * 1024 * 2 // 4
+    assert res["hbm_write_bytes"] == 2 * 8 * 1024 // 4
+
+
 def test_rocprof_script_settles_and_counts_its_calls(capsys):
     # the child runs warm-up, then untimed batches for the settle time, then
     # the measured calls, and prints the total that the parent splits the
