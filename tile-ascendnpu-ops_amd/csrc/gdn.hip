@@ -1152,8 +1152,20 @@ static int run(const bf16* q, const bf16* k, const bf16* v, const float* g, cons
   a.H = H;
   a.scale = scale;
   a.nseg = nseg;
+  // Segment 0 gets 4/5 of the others' length: in launch 1 it runs exactly
+  // on eight 16-column chains beside the map segments, and per chunk that
+  // is the slower of the two (measured at 64 heads x 128 chunks, 5
+  // segments: 256 us against 268 us with equal lengths).  Every segment
+  // keeps at least one chunk.
   for (int i = 0; i <= kMaxSeg; ++i) a.start[i] = nc;
-  for (int i = 0; i < nseg; ++i) a.start[i] = (int)((int64_t)i * nc / nseg);
+  a.start[0] = 0;
+  {
+    const int64_t wsum = 4 + 5 * (int64_t)(nseg - 1);
+    for (int i = 1; i < nseg; ++i) {
+      const int64_t at = ((int64_t)nc * (4 + 5 * (i - 1)) * 2 + wsum) / (2 * wsum);  // rounded
+      a.start[i] = (int)std::min<int64_t>(nc - (nseg - i), std::max<int64_t>(a.start[i - 1] + 1, at));
+    }
+  }
   const unsigned grid = (unsigned)(BH * std::max(nseg - 1, 1));
   if (nseg == 1) {  // every chunk exact, from h0
     a.phase = 1;
