@@ -120,7 +120,7 @@ _MANGLED = {
             "_ZN7tileops3gdn16gdn_fused_kernelILi8EEEvNS0_4ArgsE",
             "void tileops::gdn::gdn_fused_kernel<8>(tileops::gdn::Args)",
             "_ZN7tileops3gdn21gdn_copy_state_kernelEPKfPfl",
-            "_ZN7tileops3gdn18gdn_compose_kernelENS0_4ArgsE"],
+            "_ZN7tileops3gdn18gdn_compose_kernelILi2EEEvNS0_4ArgsE"],
     "gla": ["_ZN7tileops3gla17gla_decode_kernelIDF16bLb1EEEvPKT_S4_S4_S4_PKfPS2_Pfiiif"],
 }
 

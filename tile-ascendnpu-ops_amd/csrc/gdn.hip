@@ -985,31 +985,44 @@ __global__ __launch_bounds__(64 * (NCW + 4)) void gdn_fused_kernel(Args A) {
 
 // Start states of the exact segments 2 .. N-1 (between the two launches):
 // S_start(j + 1) = Phi_j S_start(j) + Bseg_j from S_start(1) = segment 0's end
-// state, one workgroup per head: wavefront w keeps columns 16 w .. of the
-// state in registers, the workgroup loads each Phi_j (as its hi and lo bf16
-// images) into LDS by direct-to-LDS loads while the product with the
-// previous one runs, and each composition is written over the columns of
-// Bseg_j it read.  LDS holds an image row r as 16 granules of 16 bytes,
+// state.  The composition is independent per state column, so each head's
+// 128 columns are split over 8 / NW workgroups of NW wavefronts (the
+// workgroups of one head on one XCD, so that its Phi images are read from
+// HBM once): wavefront w keeps 16 columns of the state in registers, the
+// workgroup loads each Phi_j (as its hi and lo bf16 images) into LDS by
+// direct-to-LDS loads while the product with the previous one runs, and
+// each composition is written over the columns of Bseg_j it read.  LDS holds an image row r as 16 granules of 16 bytes,
 // granule p at position p ^ phi_swz(r): the 16 rows one operand read
 // touches then fall in distinct bank groups.
 __device__ __forceinline__ int phi_swz(int r) { return (r & 3) | (((r >> 3) & 3) << 2); }
 
-__global__ __launch_bounds__(512) void gdn_compose_kernel(Args A) {
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void gdn_compose_kernel(Args A) {
+  constexpr int WPH = 8 / NW;  // workgroups per head
   __shared__ __attribute__((aligned(16))) bf16 phi_s[2][2 * DK * DK];  // [buf][hi | lo]
-  const int bh = blockIdx.x;
+  const int BH = A.B * A.H;
+  int bh, cq;
+  if (BH % 8 == 0) {  // workgroup i runs on XCD i % 8: a head's workgroups share it
+    const int i = blockIdx.x, l = i >> 3;
+    cq = l % WPH;
+    bh = (l / WPH) * 8 + (i & 7);
+  } else {
+    bh = blockIdx.x / WPH;
+    cq = blockIdx.x % WPH;
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, g = lane >> 4, ln = lane & 15;
-  const int col0 = 16 * wave;
+  const int col0 = 16 * (NW * cq + wave);
   const int nseg = A.nseg;
   float* const ws_head = A.ws + (size_t)bh * (2 * nseg - 3) * kStateFloats;
   auto slot = [&](int idx) { return ws_head + (size_t)idx * kStateFloats; };
   // Phi_j into image buf: 64 windows of 1 KB (four rows each; 0-31 hi,
-  // 32-63 lo), wavefront w issuing windows w, w + 8, ..
+  // 32-63 lo), wavefront w issuing windows w, w + NW, ..
   auto fetch = [&](int j, int buf) {
     const float* src = slot(1 + 2 * (j - 1));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int win = 8 * i + wave;
+    for (int i = 0; i < 64 / NW; ++i) {
+      const int win = NW * i + wave;
       const int r = 4 * (win & 31) + (lane >> 4);
       const int p = (lane & 15) ^ phi_swz(r);
       const uint32_t off = (uint32_t)((win >> 5) * DK * DK * 2 + r * DK * 2 + p * 16);
@@ -1176,7 +1189,8 @@ static int run(const bf16* q, const bf16* k, const bf16* v, const float* g, cons
   gdn_fused_kernel<8><<<dim3(grid), dim3(64 * 12), 0, s>>>(a);
   if (int e = launch_status()) return e;
   if (nseg > 2) {
-    gdn_compose_kernel<<<dim3((unsigned)BH), dim3(512), 0, s>>>(a);
+    // four workgroups of two wavefronts per head (one per CU at 64 heads)
+    gdn_compose_kernel<2><<<dim3((unsigned)(BH * 4)), dim3(128), 0, s>>>(a);
     if (int e = launch_status()) return e;
   }
   a.phase = 2;
