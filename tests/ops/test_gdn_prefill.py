@@ -99,6 +99,7 @@ def test_gdn_prefill_small(B, T, H, with_h0):
         (1, 1300, 2, 5, True),    # three maps, ragged last chunk
         (1, 1100, 1, 16, True),   # sixteen segments of one or two chunks
         (2, 700, 1, 11, False),   # eleven segments, 11 chunks (one each)
+        (2, 1100, 4, 5, True),    # 8 heads: the composition's XCD-grouped workgroups, every head
     ],
 )
 def test_gdn_prefill_segments_with_slow_decay(B, T, H, segments, with_h0):
