@@ -1110,6 +1110,10 @@ static int plan_segments(int64_t BH, int64_t nc, int requested) {
   } else {
     const int cus = device_cu_count();
     if (nc < 8 || 2 * BH > cus) return 1;
+    // at most twice the parallelism of one segment: the maps' extra work
+    // and the launches' fixed costs only pay off over long sequences
+    // (128 heads x 16 chunks: 68 us as one segment, 76 us as three)
+    if (cus / BH <= 2 && nc < 32) return 1;
     ns = (int)std::min<int64_t>(std::min<int64_t>(cus / BH + 1, nc / 4), kMaxSeg);
     if (ns < 3) ns = 1;
   }
