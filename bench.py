@@ -19,7 +19,7 @@ also carries:
                 on the host's CPU share, timed on a bounded sample
   suite         every other benchmark configuration (elementwise,
                 predicates, FusedAddLayerNorm, LogSumExp, Argmax, MHA fwd
-                causal / non-causal, GDN prefill) with its own roofline
+                causal / non-causal, GDN prefill and decode) with its own roofline
                 fraction and its own CPU-baseline figure; each row runs
                 untimed for 0.3 s (at least ``--warmup`` calls) before its
                 ``--steps`` timed calls, so that the shader clock has
@@ -274,6 +274,19 @@ def cpu_baselines(only=None) -> dict:
             f"so the full T = 8192 is extrapolated (x {8192 // T}) to {full_s:.1f} s, "
             "not measured")
         out["GatedDeltaNetPrefillFwdOp"]["full_workload_s_extrapolated"] = round(full_s, 2)
+    if want("GatedDeltaNetDecodeFwdOp"):
+        B, H, K = 16, 32, 128
+        q = F_normalize(torch.randn(B, 1, H, K, generator=gen)).bfloat16()
+        k = F_normalize(torch.randn(B, 1, H, K, generator=gen)).bfloat16()
+        v = torch.randn(B, 1, H, K, generator=gen).bfloat16()
+        g = torch.nn.functional.logsigmoid(torch.randn(B, 1, H, generator=gen))
+        beta = torch.sigmoid(torch.randn(B, 1, H, generator=gen))
+        h0 = torch.randn(B, H, K, K, generator=gen)
+        t = _median_s(lambda: tr.gdn_sequential(q, k, v, g, beta, K**-0.5, h0))
+        nbytes = B * H * (8 * K * K + 4 * K * 2 + 8)
+        out["GatedDeltaNetDecodeFwdOp"] = entry(nbytes / t / 1e9, "GB/s",
+                                                f"{B} of the 256 sequences (the token "
+                                                "recurrence on one token)")
     cores = {"threads": threads, "host_cpus": os.cpu_count(), "cpu": _cpu_model()}
     for v in out.values():
         v.update(cores)
@@ -425,6 +438,23 @@ def bench_suite(steps: int, warmup: int, only=None) -> dict:
             out[k] = v
             _log(f"{k}: {v}")
         del q, kk, vv
+
+    # GDN decode: one token for a serving batch, bf16 q, k, v, fp32 state
+    if want("GatedDeltaNetDecodeFwdOp"):
+        from tileops.ops.linear_attention import GatedDeltaNetDecodeFwdOp
+        from tileops.workloads.linear_attention import GdnDecodeWorkload
+
+        B, H, K, V = 256, 32, 128, 128
+        inputs = GdnDecodeWorkload(B, H, K, V, torch.bfloat16).gen_inputs()
+        op = GatedDeltaNetDecodeFwdOp(B, H, K, V)
+        op(*inputs)
+        k, v = _mem_entry("GatedDeltaNetDecodeFwdOp", op, [inputs], op.eval_roofline()[1], steps,
+                          warmup, "one token of 256 sequences x 32 heads: bf16 q, k "
+                          "(L2-normalised) [256, 32, 128], v [256, 32, 128]; fp32 g, beta; "
+                          "fp32 state [256, 32, 128, 128] read and a new one written")
+        out[k] = v
+        _log(f"{k}: {v}")
+        del inputs
 
     if not want("GatedDeltaNetPrefillFwdOp"):
         return out

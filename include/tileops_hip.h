@@ -286,6 +286,27 @@ int tileops_gla_decode_fwd(const void* q, const void* k, const void* v, const vo
                            const void* state, void* o, void* new_state, int64_t B, int64_t H,
                            int64_t DK, int64_t DV, float scale, int dtype, void* stream);
 
+/*
+ * Single-token gated delta rule (gated DeltaNet) decode, per (b, h):
+ *   new_state = exp(g) state + beta k (v - k^T exp(g) state)^T
+ *   o         = scale * q^T new_state
+ * (one step of the recurrence tileops_gdn_prefill_fwd runs over a sequence,
+ * on its state layout).  q, k: [B, H, DK]   v, o: [B, H, DV]  of `dtype`
+ * (F32, F16 or BF16)   g, beta: [B, H] F32 (g is the log-decay)
+ * state, new_state: [B, H, DK, DV] F32, 16-byte aligned; new_state may be
+ * state itself (the step then runs in place).  fp32 arithmetic.  DK a
+ * multiple of 32 up to 256, DV a multiple of 32 up to 4096 (TILEOPS_ESHAPE
+ * otherwise); scale finite.
+ * No reference kernel or op exists; the step is one token of
+ * golden_gdn_sequential (examples/gdn_prefill/probe/gdn_prefill_probe.py:60-77)
+ * and its interface follows GLADecodeOp.forward
+ * (tileops/ops/linear_attention/gla_decode.py:24-77) with GDN's g and beta.
+ */
+int tileops_gdn_decode_fwd(const void* q, const void* k, const void* v, const float* g,
+                           const float* beta, const float* state, void* o, float* new_state,
+                           int64_t B, int64_t H, int64_t DK, int64_t DV, float scale, int dtype,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

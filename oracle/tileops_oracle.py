@@ -333,6 +333,26 @@ def gdn_sequential(q, k, v, g, beta, h0, scale: float):
     return o.astype(np.float32), S.astype(np.float32)
 
 
+def gdn_decode(q, k, v, g, beta, state, scale: float, dtype: str):
+    """One decode step of the gated delta rule, layout BHD: the token step of
+    golden_gdn_sequential (examples/gdn_prefill/probe/gdn_prefill_probe.py:60-77)
+    on a single token,
+
+        S  = exp(g) state
+        e  = beta (v - k^T S)
+        S' = S + k e^T
+        o  = scale q^T S'
+
+    q, k: [B, H, K]; v: [B, H, V]; g, beta: [B, H]; state: [B, H, K, V].
+    float64 arithmetic; returns (o rounded once to ``dtype``, S' float32)."""
+    q, k, v, g, beta = (np.asarray(a, np.float64) for a in (q, k, v, g, beta))
+    S = np.exp(g)[:, :, None, None] * np.asarray(state, np.float64)
+    e = beta[:, :, None] * (v - np.einsum("bhk,bhkv->bhv", k, S))
+    S = S + k[:, :, :, None] * e[:, :, None, :]
+    o = scale * np.einsum("bhk,bhkv->bhv", q, S)
+    return round_to(dtype, o.astype(np.float32)), S.astype(np.float32)
+
+
 def gdn_chunked(q, k, v, g, beta, h0, scale: float, chunk: int = 64):
     """The chunked form of the same recurrence (examples/gdn_prefill/DESIGN.md:6-17),
     used only to cross-check gdn_sequential.  Per chunk (local cumulative

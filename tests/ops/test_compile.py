@@ -14,6 +14,7 @@ import pytest
 import torch
 
 from tileops.ops.attention.multi_head_attention import MultiHeadAttentionFwdOp
+from tileops.ops.linear_attention import GatedDeltaNetDecodeFwdOp
 from tileops.ops.reduction.argmax import ArgmaxFwdOp
 from tileops.ops.reduction.softmax import LogSumExpFwdOp
 
@@ -58,3 +59,20 @@ def test_argmax_compiles_to_one_graph(dtype):
     i_c = _compiled(op)(x)
     assert i_c.shape == i_e.shape and i_c.dtype == i_e.dtype
     assert torch.equal(i_c, i_e)
+
+
+@pytest.mark.gpu
+def test_gdn_decode_compiles_to_one_graph():
+    B, H, K, V = 2, 4, 128, 64
+    gen = torch.Generator().manual_seed(14)
+    q, k = (torch.nn.functional.normalize(torch.randn(B, H, K, generator=gen), dim=-1)
+            .bfloat16().cuda() for _ in range(2))
+    v = torch.randn(B, H, V, generator=gen).bfloat16().cuda()
+    g = torch.nn.functional.logsigmoid(torch.randn(B, H, generator=gen)).cuda()
+    beta = torch.sigmoid(torch.randn(B, H, generator=gen)).cuda()
+    state = torch.randn(B, H, K, V, generator=gen).cuda()
+    op = GatedDeltaNetDecodeFwdOp(B, H, K, V)
+    o_e, s_e = op(q, k, v, g, beta, state)
+    o_c, s_c = _compiled(op)(q, k, v, g, beta, state)
+    assert o_c.dtype == o_e.dtype and s_c.dtype == s_e.dtype
+    assert torch.equal(o_c, o_e) and torch.equal(s_c, s_e)

@@ -122,6 +122,8 @@ _MANGLED = {
             "_ZN7tileops3gdn21gdn_copy_state_kernelEPKfPfl",
             "_ZN7tileops3gdn18gdn_compose_kernelILi2EEEvNS0_4ArgsE"],
     "gla": ["_ZN7tileops3gla17gla_decode_kernelIDF16bLb1EEEvPKT_S4_S4_S4_PKfPS2_Pfiiif"],
+    "gdnd": ["_ZN7tileops4gdnd17gdn_decode_kernelIDF16bLi32ELi16EEEvPKT_S4_S4_PKfS6_S6_PS2_Pfif",
+             "void tileops::gdnd::gdn_decode_kernel<float, 8, 8>(float const*)"],
 }
 
 
@@ -135,6 +137,7 @@ def _kernel_groups():
     from tileops.kernels.elementwise.lerp_scalar import LerpScalarFwdKernel
     from tileops.kernels.elementwise.lerp_tensor import LerpTensorFwdKernel
     from tileops.kernels.elementwise.sub import SubFwdKernel
+    from tileops.kernels.linear_attention.gdn_decode import GDNDecodeKernel
     from tileops.kernels.linear_attention.gdn_prefill import GDNPrefillFwdKernel
     from tileops.kernels.linear_attention.gla_decode import GLADecodeKernel
     from tileops.kernels.norm.fused_add_layer_norm import FusedAddLayerNormKernel
@@ -146,10 +149,10 @@ def _kernel_groups():
             (LerpScalarFwdKernel, "bcast"), (LerpTensorFwdKernel, "bcast"),
             (BitwiseNotFwdKernel, "bitnot"), (FusedAddLayerNormKernel, "ln"),
             (LogSumExpKernel, "row"), (ArgreduceKernel, "row"), (GQAPrefillFwdKernel, "mha"),
-            (GDNPrefillFwdKernel, "gdn"), (GLADecodeKernel, "gla")]
+            (GDNPrefillFwdKernel, "gdn"), (GLADecodeKernel, "gla"), (GDNDecodeKernel, "gdnd")]
 
 
-@pytest.mark.parametrize("idx", range(14))
+@pytest.mark.parametrize("idx", range(15))
 def test_profile_regex_matches_own_kernels_only(idx):
     cls, group = _kernel_groups()[idx]
     assert cls.supported_archs == ["gfx950"], cls.__name__

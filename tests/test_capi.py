@@ -31,7 +31,8 @@ def test_header_declares_the_expected_entry_points():
     for required in ("tileops_unary_fwd", "tileops_isfp_fwd", "tileops_gated_gelu_fwd",
                      "tileops_fused_add_layernorm_fwd", "tileops_logsumexp_fwd",
                      "tileops_argreduce_fwd", "tileops_mha_fwd", "tileops_gdn_prefill_fwd",
-                     "tileops_gla_decode_fwd", "tileops_bitwise_not_fwd"):
+                     "tileops_gla_decode_fwd", "tileops_gdn_decode_fwd",
+                     "tileops_bitwise_not_fwd"):
         assert required in names
 
 
@@ -81,6 +82,18 @@ def test_host_side_argument_rejection(lib):
                                       -1.0, 1, None) == -1
     assert lib.tileops_gla_decode_fwd(None, None, None, None, None, None, None, 1, 2, 64, 64,
                                       0.1, 1, None) == -3
+    # GDN decode: DK / DV multiples of 32 (DK <= 256), a finite scale, then the
+    # null pointers, then the 16-byte alignment of the states
+    gdnd = lib.tileops_gdn_decode_fwd
+    assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 48, 64, 0.1, 2, None) == -2
+    assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 288, 64, 0.1, 2, None) == -2
+    assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 64, 80, 0.1, 2, None) == -2
+    assert gdnd(None, None, None, None, None, None, None, None, 0, 2, 64, 64, 0.1, 2, None) == -2
+    assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 64, 64,
+                float("nan"), 2, None) == -1
+    assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 64, 64, 0.1, 2, None) == -3
+    p = 4096  # non-null host values: the alignment test reads only the address
+    assert gdnd(p, p, p, p, p, p + 4, p, p, 1, 2, 64, 64, 0.1, 2, None) == -1
     # softcap: 0 is off, positive caps; negative, NaN and infinite are rejected
     assert lib.tileops_mha_fwd(None, None, None, None, None, 1, 64, 64, 2, 2, 128, 0, 1.0,
                                30.0, 2, None) == -3

@@ -444,6 +444,37 @@ def test_gdn_empty_sequence_passes_state_through():
     np.testing.assert_allclose(s, s0, rtol=1e-6)
 
 
+def test_gdn_decode_steps_equal_the_sequential_recurrence():
+    # T decode steps from h0 reproduce the token loop over the whole sequence
+    q, k, v, g, beta, s0 = _gdn_inputs(T=5)
+    o_seq, s_seq = orc.gdn_sequential(q, k, v, g, beta, s0, 0.3)
+    s = s0.astype(np.float32)
+    for t in range(q.shape[1]):
+        o, s = orc.gdn_decode(q[:, t], k[:, t], v[:, t], g[:, t], beta[:, t], s, 0.3, "float32")
+        np.testing.assert_allclose(o, o_seq[:, t], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(s, s_seq, rtol=1e-5, atol=1e-6)
+
+
+def test_gdn_decode_closed_forms():
+    *seq, s0 = _gdn_inputs(T=1)
+    q, k, v, g, beta = (a[:, 0] for a in seq)
+    # beta = 0: decay only, and the readout is exp(g) q^T state
+    o, s = orc.gdn_decode(q, k, v, g, np.zeros_like(beta), s0, 0.5, "float32")
+    np.testing.assert_allclose(s, np.exp(g)[:, :, None, None] * s0, rtol=1e-6)
+    np.testing.assert_allclose(o, 0.5 * np.exp(g)[..., None] * np.einsum("bhk,bhkv->bhv", q, s0),
+                               rtol=1e-5, atol=1e-6)
+    # beta = 1 with a unit key: the new state reads v back at k
+    o, s = orc.gdn_decode(k, k, v, g, np.ones_like(beta), s0, 1.0, "float32")
+    np.testing.assert_allclose(np.einsum("bhk,bhkv->bhv", k, s), v, atol=1e-6)
+    np.testing.assert_allclose(o, v, atol=1e-6)
+    # directions orthogonal to k keep the decayed state
+    u = np.random.default_rng(3).standard_normal(k.shape)
+    u -= np.sum(u * k, -1, keepdims=True) * k
+    np.testing.assert_allclose(np.einsum("bhk,bhkv->bhv", u, s),
+                               np.exp(g)[..., None] * np.einsum("bhk,bhkv->bhv", u, s0),
+                               rtol=1e-5, atol=1e-6)
+
+
 # -- the torch reference programs bench.py times as the CPU baseline ---------------------
 def test_torch_reference_programs_match_the_oracle():
     from oracle import torch_ref as tr

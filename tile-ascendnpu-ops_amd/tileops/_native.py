@@ -108,6 +108,11 @@ SIGNATURES = {
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float,
          _c_int, _c_p],
     ),
+    "tileops_gdn_decode_fwd": (
+        _c_int,
+        [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_float, _c_int, _c_p],
+    ),
 }
 
 _lib = None

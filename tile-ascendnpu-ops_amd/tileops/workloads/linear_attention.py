@@ -1,4 +1,4 @@
-"""Workloads of the linear-attention family: GDN prefill inputs."""
+"""Workloads of the linear-attention family: GDN prefill and decode, GLA decode."""
 
 import torch
 import torch.nn.functional as F
@@ -6,7 +6,7 @@ import torch.nn.functional as F
 from tileops.device import get_device_backend
 from tileops.workloads.workload_base import WorkloadBase
 
-__all__ = ["GdnPrefillWorkload"]
+__all__ = ["GdnDecodeWorkload", "GdnPrefillWorkload"]
 
 
 class GdnPrefillWorkload(WorkloadBase):
@@ -31,6 +31,31 @@ class GdnPrefillWorkload(WorkloadBase):
         g = F.logsigmoid(torch.randn(B, T, H, device=device))
         beta = torch.sigmoid(torch.randn(B, T, H, device=device))
         return q, k, v, g, beta
+
+
+class GdnDecodeWorkload(WorkloadBase):
+    """One decode token per head, layout BHD: q, k = L2-normalised randn,
+    v = randn (``dtype``); g = logsigmoid(randn), beta = sigmoid(randn)
+    (fp32 ``[B, H]``); state = randn (fp32 ``[B, H, K, V]``)."""
+
+    def __init__(self, batch: int, heads: int, dim_k: int, dim_v: int,
+                 dtype: torch.dtype = torch.bfloat16):
+        self.batch = batch
+        self.heads = heads
+        self.dim_k = dim_k
+        self.dim_v = dim_v
+        self.dtype = dtype
+
+    def gen_inputs(self):
+        device = get_device_backend().name
+        B, H, K, V = self.batch, self.heads, self.dim_k, self.dim_v
+        q = F.normalize(torch.randn(B, H, K, device=device), dim=-1).to(self.dtype)
+        k = F.normalize(torch.randn(B, H, K, device=device), dim=-1).to(self.dtype)
+        v = torch.randn(B, H, V, device=device).to(self.dtype)
+        g = F.logsigmoid(torch.randn(B, H, device=device))
+        beta = torch.sigmoid(torch.randn(B, H, device=device))
+        state = torch.randn(B, H, K, V, device=device)
+        return q, k, v, g, beta, state
 
 
 class GLADecodeWorkload(WorkloadBase):
