@@ -27,7 +27,7 @@ HOT_PATH_OPS = {
 }
 # ops beyond the hot path built on its kernels (the clamp kernel without an upper bound)
 WIDENED_OPS = {"AddFwdOp", "BitwiseNotFwdOp", "ClampMinFwdOp", "GLADecodeOp", "LerpFwdOp",
-               "LerpTensorFwdOp", "MishFwdOp", "SubFwdOp"}
+               "LerpTensorFwdOp", "MishFwdOp", "SubFwdOp", "GatedDeltaNetDecodeFwdOp"}
 
 
 def test_manifest_holds_the_hot_path_ops():
@@ -127,6 +127,7 @@ PINNED = [
     ("MultiHeadAttentionFwdOp", "mi355x-headline", "bfloat16", 2_199_023_255_552, 1_073_741_824),
     ("MultiHeadAttentionFwdOp", "mi355x-headline-causal", "bfloat16", 1_099_511_627_776, 1_073_741_824),
     ("GatedDeltaNetPrefillFwdOp", "mi355x-headline", "bfloat16", 95_205_105_664, 545_259_520),
+    ("GatedDeltaNetDecodeFwdOp", "mi355x-headline", "bfloat16", 948_961_280, 1_082_195_968),
 ]
 
 
@@ -153,6 +154,7 @@ def _static_ops():
     from tileops.ops.elementwise.lerp_tensor import LerpTensorFwdOp
     from tileops.ops.elementwise.mish import MishFwdOp
     from tileops.ops.elementwise.sub import SubFwdOp
+    from tileops.ops.linear_attention.gdn_decode import GatedDeltaNetDecodeFwdOp
     from tileops.ops.linear_attention.gdn_prefill import GatedDeltaNetPrefillFwdOp
     from tileops.ops.linear_attention.gla_decode import GLADecodeOp
 
@@ -196,6 +198,8 @@ def _static_ops():
             weight=tuple(w["input_shape"]), dtype=dt),
         "GatedDeltaNetPrefillFwdOp": lambda w, dt: GatedDeltaNetPrefillFwdOp(
             w["batch"], w["seq_len"], w["heads"], w["dim_k"], w["dim_v"], dtype=dt),
+        "GatedDeltaNetDecodeFwdOp": lambda w, dt: GatedDeltaNetDecodeFwdOp(
+            w["batch"], w["heads"], w["dim_k"], w["dim_v"], dtype=dt),
     }
 
 
