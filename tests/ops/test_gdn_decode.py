@@ -7,12 +7,11 @@ tests/test_oracle_pins.py against the token loop and closed forms.  Inputs
 are exact in their storage dtypes; the kernel computes in fp32, the oracle in
 fp64.  Tolerances: the fp32 state at rtol = atol = 2e-5 (fp32 rounding of
 K-term sums); o at one unit in the last place of its dtype (rtol 8e-3 bf16,
-1e-3 fp16, 2e-5 fp32), since both sides round once to it.  Shapes cover the
-three row-slice widths the kernel picks (32, 16 and 8 packs of 4 columns:
-whole 128-column rows, then narrower slices where the value width or the
-rows per thread demand them), K = 32 .. 256, value widths from one 32-column
-block to the 4096 maximum, several batches and heads, a custom scale, and the
-serving shape; a chained test runs a prefill and continues it with decode
+1e-3 fp16, 2e-5 fp32), since both sides round once to it.  Shapes cover both
+row-slice widths the kernel picks (16 packs of 4 columns where they divide
+the value width, else 8), K = 32 .. 256 (1 to 16 rows per thread), value
+widths from one 32-column block to the 4096 maximum, several batches and
+heads, a custom scale, and the serving shape; a chained test runs a prefill and continues it with decode
 steps, and the C-ABI's in-place form must equal the out-of-place one bit for
 bit.
 """
@@ -47,8 +46,9 @@ _CASES = [
     (1, 2, 160, 1024, _F32, None, "k160-v1024"),
     (3, 5, 224, 96, _BF16, None, "k224-v96"),
     (2, 2, 192, 4096, _BF16, None, "k192-v4096-max"),
-    (2, 3, 64, 256, _F16, None, "k64-v256"),
     (1, 4, 96, 384, _F32, None, "k96-v384"),
+    (2, 2, 32, 64, _F32, None, "k32-v64"),
+    (1, 3, 224, 128, _F16, None, "k224-v128"),
 ]
 
 

@@ -122,7 +122,7 @@ _MANGLED = {
             "_ZN7tileops3gdn21gdn_copy_state_kernelEPKfPfl",
             "_ZN7tileops3gdn18gdn_compose_kernelILi2EEEvNS0_4ArgsE"],
     "gla": ["_ZN7tileops3gla17gla_decode_kernelIDF16bLb1EEEvPKT_S4_S4_S4_PKfPS2_Pfiiif"],
-    "gdnd": ["_ZN7tileops4gdnd17gdn_decode_kernelIDF16bLi32ELi16EEEvPKT_S4_S4_PKfS6_S6_PS2_Pfif",
+    "gdnd": ["_ZN7tileops4gdnd17gdn_decode_kernelIDF16bLi16ELi8EEEvPKT_S4_S4_PKfS6_S6_PS2_Pfif",
              "void tileops::gdnd::gdn_decode_kernel<float, 8, 8>(float const*)"],
 }
 

@@ -91,8 +91,8 @@ class GDNDecodeKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # gdn_decode_kernel: 256-thread workgroups, each over 128 value columns
-        # of a head where dim_v and dim_k allow it (else 64 or 32)
+        # gdn_decode_kernel: 256-thread workgroups, each over 64 value columns
+        # of a head where dim_v allows it (else 32)
         return {"threads": 256}
 
     def forward(
