@@ -2,11 +2,14 @@
 
 The reference has no GDN Op or test (it was not delivered); the oracle is the
 restated golden_gdn_sequential (examples/gdn_prefill/probe/gdn_prefill_probe.py:60-77).
-Output and final state are compared with the half-precision bound
-rtol = atol = 1e-2 (the state is fp32, but every product that forms it takes
-bf16 operands, as the reference's chunked form does); every check prints the
-largest error of o and of the state as a fraction of that bound, so that the
-margin is on record in the test log.  Shapes cover ragged sequence lengths,
+The bf16 output o is compared with the half-precision bound rtol = atol =
+1e-2.  The fp32 final state, every product of which takes bf16 operands (as
+the reference's chunked form does), is compared at rtol = atol = 5e-3 (the
+largest error recorded over these cases is 0.19 of 1e-2), and at 1e-2 under
+slow decay, where the state carries across a thousand tokens and several
+composed segment maps (largest recorded error 0.54 of 1e-2).  Every check
+prints the largest error of o and of the state as a fraction of its bound,
+so that the margin is on record in the test log.  Shapes cover ragged sequence lengths,
 an initial state, several heads, forced segment counts (the sequence split
 into segments whose state maps are composed) with slow decay, so that the
 maps carry the state across many chunks, and, on sampled heads, the full
@@ -24,15 +27,16 @@ from tileops.kernels.linear_attention.gdn_prefill import GDNPrefillFwdKernel
 from tileops.ops.linear_attention import GatedDeltaNetPrefillFwdOp
 from tileops.workloads.linear_attention import GdnPrefillWorkload
 
-TOL = 1e-2
+TOL = 1e-2  # o (bf16), and the state under slow decay
+STATE_TOL = 5e-3  # the fp32 state at the workload's decay
 
 
-def _frac(got, ref):
-    """Largest |got - ref| / (TOL + TOL |ref|): 1.0 is the bound."""
-    return float(np.max(np.abs(got - ref) / (TOL + TOL * np.abs(ref)))) if ref.size else 0.0
+def _frac(got, ref, tol=TOL):
+    """Largest |got - ref| / (tol + tol |ref|): 1.0 is the bound."""
+    return float(np.max(np.abs(got - ref) / (tol + tol * np.abs(ref)))) if ref.size else 0.0
 
 
-def _check(inputs, o, hT, h0, scale, pairs, label=""):
+def _check(inputs, o, hT, h0, scale, pairs, label="", state_tol=STATE_TOL):
     q, k, v, g, beta = (to_np(t) for t in inputs)
     s0 = None if h0 is None else to_np(h0)
     worst_o = worst_s = 0.0
@@ -45,9 +49,9 @@ def _check(inputs, o, hT, h0, scale, pairs, label=""):
         o_ref = orc.round_to("bfloat16", o_ref)
         got_o, got_s = to_np(o)[sl], to_np(hT)[b:b + 1, h:h + 1]
         worst_o = max(worst_o, _frac(got_o, o_ref))
-        worst_s = max(worst_s, _frac(got_s, h_ref))
+        worst_s = max(worst_s, _frac(got_s, h_ref, state_tol))
         assert_close_np(got_o, o_ref, TOL, TOL, f"o b{b} h{h}")
-        assert_close_np(got_s, h_ref, TOL, TOL, f"state b{b} h{h}")
+        assert_close_np(got_s, h_ref, state_tol, state_tol, f"state b{b} h{h}")
     print(f"[gdn {label}] largest error / bound: o {worst_o:.3f}, state {worst_s:.3f}")
     return worst_o, worst_s
 
@@ -110,7 +114,7 @@ def test_gdn_prefill_segments_with_slow_decay(B, T, H, segments, with_h0):
                                config={"segments": segments})
     o, hT = kern(*inputs, h0)
     _check(inputs, o, hT, h0, 128**-0.5, [(b, h) for b in range(B) for h in range(H)],
-           f"B{B} T{T} H{H} {segments} segments, slow decay")
+           f"B{B} T{T} H{H} {segments} segments, slow decay", state_tol=TOL)
     # one segment (no maps) agrees within the same bound
     o1, hT1 = GDNPrefillFwdKernel(B, T, H, 128, 128, 64, torch.bfloat16,
                                   config={"segments": 1})(*inputs, h0)
