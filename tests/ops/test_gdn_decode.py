@@ -120,6 +120,22 @@ def test_gdn_decode_in_place_equals_out_of_place(dtype):
     assert torch.equal(state, ns) and torch.equal(o2, o)
 
 
+@pytest.mark.gpu
+def test_gdn_decode_misaligned_state_view():
+    # a contiguous state view 4 bytes past a 16-byte boundary is realigned
+    B, H, K, V = 1, 2, 32, 64
+    torch.manual_seed(8)
+    q, k, v, g, beta, state = GdnDecodeWorkload(B, H, K, V, _F32).gen_inputs()
+    flat = torch.empty(state.numel() + 1, device=state.device)
+    shifted = flat[1:].view(B, H, K, V)
+    shifted.copy_(state)
+    assert shifted.data_ptr() % 16 == 4
+    op = GatedDeltaNetDecodeFwdOp(B, H, K, V, dtype=_F32)
+    o, ns = op(q, k, v, g, beta, shifted)
+    o_ref, ns_ref = op(q, k, v, g, beta, state)
+    assert torch.equal(o, o_ref) and torch.equal(ns, ns_ref)
+
+
 @pytest.mark.smoke
 def test_gdn_decode_default_scale_and_roofline():
     op = GatedDeltaNetDecodeFwdOp(2, 4, 128, 64, dtype=_F16)

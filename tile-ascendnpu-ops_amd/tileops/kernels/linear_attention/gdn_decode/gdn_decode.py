@@ -114,4 +114,6 @@ class GDNDecodeKernel(Kernel):
             if t.dtype != dt:
                 raise ValueError(f"Expected {name}.dtype {dt}, got {t.dtype}")
         q, k, v, g, beta, state = (t.contiguous() for t in (q, k, v, g, beta, state))
+        if state.data_ptr() % 16:  # the kernel moves the state in 16-byte packs
+            state = state.clone()
         return _gdn_decode_fwd(B, H, K, V, self.scale, q, k, v, g, beta, state)
