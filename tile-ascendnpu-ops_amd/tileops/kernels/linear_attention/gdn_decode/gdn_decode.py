@@ -27,6 +27,8 @@ def _gdn_decode_fwd(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
     state: torch.Tensor,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
+    if state.data_ptr() % 16:  # the kernel moves the state in 16-byte packs
+        state = state.clone()
     o = torch.empty_like(v)
     new_state = torch.empty_like(state)
     code = _native.lib().tileops_gdn_decode_fwd(
@@ -114,6 +116,4 @@ class GDNDecodeKernel(Kernel):
             if t.dtype != dt:
                 raise ValueError(f"Expected {name}.dtype {dt}, got {t.dtype}")
         q, k, v, g, beta, state = (t.contiguous() for t in (q, k, v, g, beta, state))
-        if state.data_ptr() % 16:  # the kernel moves the state in 16-byte packs
-            state = state.clone()
         return _gdn_decode_fwd(B, H, K, V, self.scale, q, k, v, g, beta, state)
