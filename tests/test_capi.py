@@ -89,6 +89,8 @@ def test_host_side_argument_rejection(lib):
     assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 288, 64, 0.1, 2, None) == -2
     assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 64, 80, 0.1, 2, None) == -2
     assert gdnd(None, None, None, None, None, None, None, None, 0, 2, 64, 64, 0.1, 2, None) == -2
+    assert gdnd(None, None, None, None, None, None, None, None, 1 << 20, 1 << 20, 64, 64, 0.1, 2,
+                None) == -2  # more workgroups than a grid holds
     assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 64, 64,
                 float("nan"), 2, None) == -1
     assert gdnd(None, None, None, None, None, None, None, None, 1, 2, 64, 64, 0.1, 2, None) == -3

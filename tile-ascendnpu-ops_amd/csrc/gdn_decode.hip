@@ -191,11 +191,10 @@ extern "C" int tileops_gdn_decode_fwd(const void* q, const void* k, const void* 
                                       const float* beta, const float* state, void* o,
                                       float* new_state, int64_t B, int64_t H, int64_t DK,
                                       int64_t DV, float scale, int dtype, void* stream) {
-  if (B <= 0 || H <= 0) return TILEOPS_ESHAPE;
+  if (B <= 0 || H <= 0 || B > INT32_MAX || H > INT32_MAX) return TILEOPS_ESHAPE;
   if (DK <= 0 || DK % 32 != 0 || DK > gdnd::kMaxDK || DV <= 0 || DV % 32 != 0 || DV > 4096)
     return TILEOPS_ESHAPE;
-  if (B * H * (DV / 32) > (int64_t)UINT32_MAX || B * H > INT64_MAX / (DK * DV))
-    return TILEOPS_ESHAPE;
+  if (B * H > INT32_MAX / (DV / 32)) return TILEOPS_ESHAPE;  // grid size
   if (!(scale > -INFINITY && scale < INFINITY)) return TILEOPS_EINVAL;  // NaN too
   if (!q || !k || !v || !g || !beta || !state || !o || !new_state) return TILEOPS_ENULL;
   if (!host_aligned16(state) || !host_aligned16(new_state)) return TILEOPS_EINVAL;
