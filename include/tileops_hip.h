@@ -295,8 +295,8 @@ int tileops_gla_decode_fwd(const void* q, const void* k, const void* v, const vo
  * (F32, F16 or BF16)   g, beta: [B, H] F32 (g is the log-decay)
  * state, new_state: [B, H, DK, DV] F32, 16-byte aligned; new_state may be
  * state itself (the step then runs in place).  fp32 arithmetic.  DK a
- * multiple of 32 up to 256, DV a multiple of 32 up to 4096 (TILEOPS_ESHAPE
- * otherwise); scale finite.
+ * multiple of 32 up to 256, DV a multiple of 32 up to 4096, B * H * DV / 32
+ * at most 2^31 - 1 (TILEOPS_ESHAPE otherwise); scale finite.
  * No reference kernel or op exists; the step is one token of
  * golden_gdn_sequential (examples/gdn_prefill/probe/gdn_prefill_probe.py:60-77)
  * and its interface follows GLADecodeOp.forward
