@@ -19,7 +19,8 @@ from tileops.workloads.linear_attention import GLADecodeWorkload, gla_decode_tol
 _F16, _BF16, _F32 = torch.float16, torch.bfloat16, torch.float32
 
 # (B, H, DK, DV, dtype, scale, id) -- the reference's cases, plus DV = 200
-# (no 16-byte column groups: the element-wise path)
+# (no 16-byte column groups: the element-wise path) and three shapes of the
+# row-slice kernel (16-, 16- over two workgroups, and 4-pack slices)
 _CASES = [
     (2, 4, 64, 64, _F16, -1.0, "smoke-d64-fp16"),
     (2, 4, 64, 64, _BF16, -1.0, "smoke-d64-bf16"),
@@ -31,6 +32,10 @@ _CASES = [
     (1, 4, 128, 64, _F16, -1.0, "rect-d128x64"),
     (2, 3, 64, 64, _BF16, 0.25, "custom-scale"),
     (1, 3, 48, 200, _F16, -1.0, "dv200-elementwise"),
+    # the row-slice kernel at its other slice widths and rows per thread
+    (2, 3, 256, 256, _BF16, -1.0, "rows-k256-v256"),
+    (1, 4, 128, 128, _F32, -1.0, "rows-f32-two-slices"),
+    (2, 2, 64, 32, _BF16, -1.0, "rows-4-pack-slices"),
 ]
 
 

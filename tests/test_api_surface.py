@@ -121,7 +121,8 @@ _MANGLED = {
             "void tileops::gdn::gdn_fused_kernel<8>(tileops::gdn::Args)",
             "_ZN7tileops3gdn21gdn_copy_state_kernelEPKfPfl",
             "_ZN7tileops3gdn18gdn_compose_kernelILi2EEEvNS0_4ArgsE"],
-    "gla": ["_ZN7tileops3gla17gla_decode_kernelIDF16bLb1EEEvPKT_S4_S4_S4_PKfPS2_Pfiiif"],
+    "gla": ["_ZN7tileops3gla17gla_decode_kernelIDF16bLb1EEEvPKT_S4_S4_S4_PKfPS2_Pfiiif",
+            "_ZN7tileops3gla22gla_decode_rows_kernelIDF16bLi16ELi8EEEvPKT_S4_S4_S4_S4_PS2_S5_if"],
     "gdnd": ["_ZN7tileops4gdnd17gdn_decode_kernelIDF16bLi16ELi8EEEvPKT_S4_S4_PKfS6_S6_PS2_Pfif",
              "void tileops::gdnd::gdn_decode_kernel<float, 8, 8>(float const*)"],
 }

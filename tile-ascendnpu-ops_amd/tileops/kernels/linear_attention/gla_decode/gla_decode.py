@@ -6,8 +6,9 @@ config)``, a non-positive ``scale`` meaning ``DK ** -0.5``, ``forward(q, k, v,
 gk, state) -> (o, new_state)``) and the golden golden_gla_decode
 (gla_decode_kernel/_gla_decode_kernel.py:211-218).  Layout BHD: q, k, gk
 ``[B, H, DK]``, v ``[B, H, DV]``, state ``[B, H, DK, DV]``, all one dtype.
-Device code: gla_decode_kernel in csrc/gla.hip.  ``k_tile`` is accepted for
-interface parity; the HIP kernel streams whole rows and needs no tiling.
+Device code: gla_decode_rows_kernel (16-byte row slices, the common shapes)
+or gla_decode_kernel in csrc/gla.hip.  ``k_tile`` is accepted for interface
+parity; the HIP kernels stream whole rows and need no tiling.
 """
 
 from typing import Optional, Tuple
@@ -54,7 +55,7 @@ class GLADecodeKernel(Kernel):
     """
 
     SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
-    profile_kernel_name = r"gla(?:::|\d+)gla_decode_kernel"
+    profile_kernel_name = r"gla(?:::|\d+)gla_decode_(?:rows_)?kernel"
 
     def __init__(
         self,
@@ -86,7 +87,7 @@ class GLADecodeKernel(Kernel):
 
     @property
     def default_config(self) -> dict:
-        # gla_decode_kernel: one 256-thread workgroup per (batch, head)
+        # 256-thread workgroups, one or more per (batch, head)
         return {"threads": 256}
 
     def forward(
