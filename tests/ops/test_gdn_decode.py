@@ -11,9 +11,10 @@ K-term sums); o at one unit in the last place of its dtype (rtol 8e-3 bf16,
 row-slice widths the kernel picks (16 packs of 4 columns where they divide
 the value width, else 8), K = 32 .. 256 (1 to 16 rows per thread), value
 widths from one 32-column block to the 4096 maximum, several batches and
-heads, a custom scale, and the serving shape; a chained test runs a prefill and continues it with decode
-steps, and the C-ABI's in-place form must equal the out-of-place one bit for
-bit.
+heads, a custom scale, the serving shape, and a state over 128 MiB (read
+with non-temporal loads); a chained test runs a prefill and continues it
+with decode steps, and the C-ABI's in-place form must equal the
+out-of-place one bit for bit.
 """
 
 import ctypes
@@ -49,6 +50,7 @@ _CASES = [
     (1, 4, 96, 384, _F32, None, "k96-v384"),
     (2, 2, 32, 64, _F32, None, "k32-v64"),
     (1, 3, 224, 128, _F16, None, "k224-v128"),
+    (66, 32, 128, 128, _BF16, None, "state-over-128MiB-nontemporal-loads"),
 ]
 
 

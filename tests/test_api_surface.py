@@ -122,8 +122,8 @@ _MANGLED = {
             "_ZN7tileops3gdn21gdn_copy_state_kernelEPKfPfl",
             "_ZN7tileops3gdn18gdn_compose_kernelILi2EEEvNS0_4ArgsE"],
     "gla": ["_ZN7tileops3gla17gla_decode_kernelIDF16bLb1EEEvPKT_S4_S4_S4_PKfPS2_Pfiiif",
-            "_ZN7tileops3gla22gla_decode_rows_kernelIDF16bLi16ELi8EEEvPKT_S4_S4_S4_S4_PS2_S5_if"],
-    "gdnd": ["_ZN7tileops4gdnd17gdn_decode_kernelIDF16bLi16ELi8EEEvPKT_S4_S4_PKfS6_S6_PS2_Pfif",
+            "_ZN7tileops3gla22gla_decode_rows_kernelIDF16bLi16ELi8ELb0EEEvPKT_S4_S4_S4_S4_PS2_S5_if"],
+    "gdnd": ["_ZN7tileops4gdnd17gdn_decode_kernelIDF16bLi16ELi8ELb1EEEvPKT_S4_S4_PKfS6_S6_PS2_Pfif",
              "void tileops::gdnd::gdn_decode_kernel<float, 8, 8>(float const*)"],
 }
 

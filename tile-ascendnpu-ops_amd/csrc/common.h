@@ -98,6 +98,12 @@ inline int device_cu_count() {
   return cached[dev];
 }
 
+// A streamed operand up to this size may still sit in the 256 MB Infinity
+// Cache when it is read again soon (a decode loop over a small model, a
+// repeated call): kernels read such operands with plain loads and larger
+// ones, which cannot stay resident, with non-temporal loads.
+constexpr int64_t kCacheFitBytes = int64_t(128) << 20;
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : (int)e;

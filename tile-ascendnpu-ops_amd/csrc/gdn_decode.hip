@@ -21,7 +21,9 @@
 // (CG = 32) it is 2-3 % faster on large batches and 20-27 % faster on
 // small ones, whose heads alone do not fill the GPU.  The column sums
 // meet by lane swaps inside a wavefront and LDS between the four.  The state
-// is read and written once (non-temporal: it is not reused by this step).
+// is read and written once: non-temporal stores, and non-temporal loads when
+// the state of the call exceeds what the Infinity Cache could keep (128 MiB;
+// a smaller state read again soon may still be there).
 // All reads of the state precede the barrier that all its writes follow, and
 // each element is read and written by the same thread, so the new state may
 // overwrite the old in place.
@@ -43,8 +45,10 @@ __device__ __forceinline__ f32x4 xor_sum4(f32x4 a, int mask) {
   return a;
 }
 
-// CG 16-byte column packs per row slice, RPT rows per thread (DK = RPT * 256 / CG)
-template <typename T, int CG, int RPT>
+// CG 16-byte column packs per row slice, RPT rows per thread (DK = RPT * 256 /
+// CG); NTL: non-temporal state loads (a template parameter: the compiler
+// merges a runtime choice between the two load forms into plain loads)
+template <typename T, int CG, int RPT, bool NTL>
 __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const float* state, T* o,
@@ -61,13 +65,20 @@ __global__ __launch_bounds__(kThreads) void gdn_decode_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cg = tid % CG, rg = tid / CG;
 
-  // this thread's rows of its four columns, issued first
+  // this thread's rows of its four columns, issued first (non-temporal
+  // when the state is too large to stay in the caches)
   const float* S = state + bh * DK * DV + c0 + 4 * cg;
   f32x4 sv[RPT];
+  if constexpr (NTL) {
 #pragma unroll
-  for (int i = 0; i < RPT; ++i)
-    sv[i] = __builtin_nontemporal_load(
-        reinterpret_cast<const f32x4*>(S + (int64_t)(rg + RG * i) * DV));
+    for (int i = 0; i < RPT; ++i)
+      sv[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4*>(S + (int64_t)(rg + RG * i) * DV));
+  } else {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      sv[i] = *reinterpret_cast<const f32x4*>(S + (int64_t)(rg + RG * i) * DV);
+  }
   // q, k as fp32 in LDS, and q . k
   float qk = 0.0f;
   for (int r = tid; r < DK; r += kThreads) {
@@ -144,9 +155,16 @@ template <typename T, int CG, int KB>
 static bool launch(const Launch& L) {
   if constexpr (KB * CG / 8 <= kMaxRPT) {
     const dim3 grid((unsigned)(L.BH * (L.DV / (4 * CG)))), block(kThreads);
-    gdn_decode_kernel<T, CG, KB * CG / 8><<<grid, block, 0, L.s>>>(
-        static_cast<const T*>(L.q), static_cast<const T*>(L.k), static_cast<const T*>(L.v), L.g,
-        L.beta, L.state, static_cast<T*>(L.o), L.new_state, L.DV, L.scale);
+    const T* q = static_cast<const T*>(L.q);
+    const T* k = static_cast<const T*>(L.k);
+    const T* v = static_cast<const T*>(L.v);
+    T* o = static_cast<T*>(L.o);
+    if (L.BH * (32 * KB) * L.DV * 4 > kCacheFitBytes)
+      gdn_decode_kernel<T, CG, KB * CG / 8, true><<<grid, block, 0, L.s>>>(
+          q, k, v, L.g, L.beta, L.state, o, L.new_state, L.DV, L.scale);
+    else
+      gdn_decode_kernel<T, CG, KB * CG / 8, false><<<grid, block, 0, L.s>>>(
+          q, k, v, L.g, L.beta, L.state, o, L.new_state, L.DV, L.scale);
     return true;
   } else {
     return false;

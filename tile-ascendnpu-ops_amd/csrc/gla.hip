@@ -15,11 +15,11 @@
 //   issues the loads of all its RPT rows before anything else, exp(gk), k
 //   and q are formed once per row in LDS, the new state goes out by
 //   non-temporal stores, and the readout partials meet by lane swaps and
-//   LDS.  The state loads stay plain: a state read again soon (a decode
-//   loop that fits the caches) then hits in them, and a cold one costs
-//   2-5 % against non-temporal loads.  Measured against the general kernel
-//   below at B8 H64 / B8 H32, bf16 K = V = 128, state cold: 7.13 / 4.73 us
-//   against 8.76 / 6.31 (back-to-back launches).
+//   LDS.  The state loads are plain up to 128 MiB of state (a state read
+//   again soon may then hit in the Infinity Cache; a cold one costs 2-5 %
+//   against non-temporal loads) and non-temporal beyond.  Measured against
+//   the general kernel below at B8 H64 / B8 H32, bf16 K = V = 128, state
+//   cold: 7.13 / 4.73 us against 8.76 / 6.31 (back-to-back launches).
 // - gla_decode_kernel (any shape): one workgroup per (b, h); a thread owns
 //   VEC consecutive value columns (16 bytes when the row allows it) of rows
 //   rg, rg + RG, ...; consecutive threads cover a row left to right, so
@@ -95,8 +95,10 @@ __global__ __launch_bounds__(kThreads) void gla_decode_kernel(
   }
 }
 
-// CG 16-byte packs per row slice, RPT rows per thread (DK = RPT * 256 / CG)
-template <typename T, int CG, int RPT>
+// CG 16-byte packs per row slice, RPT rows per thread (DK = RPT * 256 / CG);
+// NTL: non-temporal state loads (a template parameter: the compiler merges a
+// runtime choice between the two load forms into plain loads)
+template <typename T, int CG, int RPT, bool NTL>
 __global__ __launch_bounds__(kThreads) void gla_decode_rows_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ gk, const T* __restrict__ state, T* __restrict__ o,
@@ -116,9 +118,16 @@ __global__ __launch_bounds__(kThreads) void gla_decode_rows_kernel(
 
   const T* S = state + bh * DK * DV + c0 + VEC * cg;
   u32x4 sv[RPT];
+  if constexpr (NTL) {
 #pragma unroll
-  for (int i = 0; i < RPT; ++i)
-    sv[i] = *reinterpret_cast<const u32x4*>(S + (int64_t)(rg + RG * i) * DV);
+    for (int i = 0; i < RPT; ++i)
+      sv[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(S + (int64_t)(rg + RG * i) * DV));
+  } else {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      sv[i] = *reinterpret_cast<const u32x4*>(S + (int64_t)(rg + RG * i) * DV);
+  }
   for (int r = tid; r < DK; r += kThreads) {
     dec[r] = expf(Elem<T>::to_f32(gk[bh * DK + r]));
     ks[r] = Elem<T>::to_f32(k[bh * DK + r]);
@@ -174,11 +183,17 @@ __global__ __launch_bounds__(kThreads) void gla_decode_rows_kernel(
 template <typename T, int CG, int RPT>
 static void launch_rows(const void* q, const void* k, const void* v, const void* gk,
                         const void* state, void* o, void* ns, int64_t nblk, int DV, float scale,
-                        hipStream_t s) {
-  gla_decode_rows_kernel<T, CG, RPT><<<dim3((unsigned)nblk), dim3(kThreads), 0, s>>>(
-      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-      static_cast<const T*>(gk), static_cast<const T*>(state), static_cast<T*>(o),
-      static_cast<T*>(ns), DV, scale);
+                        bool stream_in, hipStream_t s) {
+  const T *qt = static_cast<const T*>(q), *kt = static_cast<const T*>(k);
+  const T *vt = static_cast<const T*>(v), *gt = static_cast<const T*>(gk);
+  const T* st = static_cast<const T*>(state);
+  T *ot = static_cast<T*>(o), *nt = static_cast<T*>(ns);
+  if (stream_in)
+    gla_decode_rows_kernel<T, CG, RPT, true><<<dim3((unsigned)nblk), dim3(kThreads), 0, s>>>(
+        qt, kt, vt, gt, st, ot, nt, DV, scale);
+  else
+    gla_decode_rows_kernel<T, CG, RPT, false><<<dim3((unsigned)nblk), dim3(kThreads), 0, s>>>(
+        qt, kt, vt, gt, st, ot, nt, DV, scale);
 }
 
 // The rows kernel where the shape allows it: 16-byte packs, a row slice of
@@ -192,12 +207,13 @@ static bool try_rows(const void* q, const void* k, const void* v, const void* gk
   if (DK % RG != 0) return false;
   const int64_t nblk = BH * (DV / (VEC * CG));
   if (nblk > INT32_MAX) return false;
+  const bool si = BH * DK * DV * (int64_t)sizeof(T) > kCacheFitBytes;
   switch (DK / RG) {
-    case 1: launch_rows<T, CG, 1>(q, k, v, gk, state, o, ns, nblk, DV, scale, s); return true;
-    case 2: launch_rows<T, CG, 2>(q, k, v, gk, state, o, ns, nblk, DV, scale, s); return true;
-    case 4: launch_rows<T, CG, 4>(q, k, v, gk, state, o, ns, nblk, DV, scale, s); return true;
-    case 8: launch_rows<T, CG, 8>(q, k, v, gk, state, o, ns, nblk, DV, scale, s); return true;
-    case 16: launch_rows<T, CG, 16>(q, k, v, gk, state, o, ns, nblk, DV, scale, s); return true;
+    case 1: launch_rows<T, CG, 1>(q, k, v, gk, state, o, ns, nblk, DV, scale, si, s); return true;
+    case 2: launch_rows<T, CG, 2>(q, k, v, gk, state, o, ns, nblk, DV, scale, si, s); return true;
+    case 4: launch_rows<T, CG, 4>(q, k, v, gk, state, o, ns, nblk, DV, scale, si, s); return true;
+    case 8: launch_rows<T, CG, 8>(q, k, v, gk, state, o, ns, nblk, DV, scale, si, s); return true;
+    case 16: launch_rows<T, CG, 16>(q, k, v, gk, state, o, ns, nblk, DV, scale, si, s); return true;
   }
   return false;
 }
