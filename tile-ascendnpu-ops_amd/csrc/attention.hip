@@ -621,9 +621,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     if (ntiles > 0) {
       const int t = ntiles - 1;
-      softmax(t);
+      // a last tile wholly above this wavefront's rows adds nothing (as in
+      // the two-slot schedule below)
+      const bool live = !CAUSAL || t * BN <= q0 + wave * 32 + 31 + off;
+      if (live) softmax(t);
       lds_barrier();
-      mfma_phase(yes(), no(), ld_none(), t % 3, 0, -1);
+      if (live) mfma_phase(yes(), no(), ld_none(), t % 3, 0, -1);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
     }
@@ -685,10 +688,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     if (ntiles > 0) {
       const int t = ntiles - 1;
-      softmax(t);
+      // Under a causal mask the last tile can lie wholly above this
+      // wavefront's rows (group A's 128 rows against the block's last 128
+      // keys): its probabilities are all 0, so its softmax and P V add
+      // nothing and are skipped (S(t) was formed, unused; every barrier and
+      // wait is kept).
+      const bool live = !CAUSAL || t * BN <= q0 + wave * 32 + 31 + off;
+      if (live) softmax(t);
       __builtin_amdgcn_s_waitcnt(0x0F70);
       lds_barrier();
-      mfma_phase(yes(), no(), ld_none(), t % 2, 0, -1);
+      if (live) mfma_phase(yes(), no(), ld_none(), t % 2, 0, -1);
       lds_barrier();
     }
     lds_barrier();  // softmax phase of step ntiles (nothing left to do)
