@@ -456,22 +456,19 @@ def bench_suite(steps: int, warmup: int, only=None) -> dict:
 
     if not want("GatedDeltaNetPrefillFwdOp"):
         return out
-    try:
-        from tileops.ops.linear_attention import GatedDeltaNetPrefillFwdOp
-        from tileops.workloads.linear_attention import GdnPrefillWorkload
+    from tileops.ops.linear_attention import GatedDeltaNetPrefillFwdOp
+    from tileops.workloads.linear_attention import GdnPrefillWorkload
 
-        wl = GdnPrefillWorkload(4, 8192, 16, 128, 128, torch.bfloat16)
-        inputs = wl.gen_inputs()
-        op = GatedDeltaNetPrefillFwdOp(4, 8192, 16, 128, 128, chunk_size=64)
-        flops, nbytes = op.eval_roofline()
-        k, v = _mfma_entry("GatedDeltaNetPrefillFwdOp", op, [inputs], flops, steps, warmup,
-                           "bf16 q, k (L2-normalised), v [4, 8192, 16, 128]; fp32 g, beta; "
-                           "chunk 64, zero initial state")
-        v["GB/s"] = round(nbytes / (v["ms"] * 1e-3) / 1e9, 1)
-        out[k] = v
-        _log(f"{k}: {v}")
-    except (ImportError, RuntimeError) as e:  # GDN op not built yet
-        out["GatedDeltaNetPrefillFwdOp"] = {"status": f"not measured: {e}"}
+    wl = GdnPrefillWorkload(4, 8192, 16, 128, 128, torch.bfloat16)
+    inputs = wl.gen_inputs()
+    op = GatedDeltaNetPrefillFwdOp(4, 8192, 16, 128, 128, chunk_size=64)
+    flops, nbytes = op.eval_roofline()
+    k, v = _mfma_entry("GatedDeltaNetPrefillFwdOp", op, [inputs], flops, steps, warmup,
+                       "bf16 q, k (L2-normalised), v [4, 8192, 16, 128]; fp32 g, beta; "
+                       "chunk 64, zero initial state")
+    v["GB/s"] = round(nbytes / (v["ms"] * 1e-3) / 1e9, 1)
+    out[k] = v
+    _log(f"{k}: {v}")
     return out
 
 
