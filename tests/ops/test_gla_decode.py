@@ -21,7 +21,7 @@ _F16, _BF16, _F32 = torch.float16, torch.bfloat16, torch.float32
 # (B, H, DK, DV, dtype, scale, id) -- the reference's cases, plus DV = 200
 # (no 16-byte column groups: the element-wise path) and three shapes of the
 # row-slice kernel (16-, 16- over two workgroups, and 4-pack slices), and one
-# whose state exceeds 128 MiB (non-temporal state loads)
+# bf16 and one fp32 whose state exceeds 128 MiB (non-temporal state loads)
 _CASES = [
     (2, 4, 64, 64, _F16, -1.0, "smoke-d64-fp16"),
     (2, 4, 64, 64, _BF16, -1.0, "smoke-d64-bf16"),
@@ -38,6 +38,7 @@ _CASES = [
     (1, 4, 128, 128, _F32, -1.0, "rows-f32-two-slices"),
     (2, 2, 64, 32, _BF16, -1.0, "rows-4-pack-slices"),
     (64, 66, 128, 128, _BF16, -1.0, "rows-state-over-128MiB"),
+    (32, 66, 128, 128, _F32, -1.0, "rows-f32-state-over-128MiB"),
 ]
 
 
