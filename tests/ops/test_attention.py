@@ -89,7 +89,8 @@ def test_mha_fwd(batch, seq_len, heads, dim, causal, dtype):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("sq, skv", [(256, 256), (200, 333), (64, 1024)])
+@pytest.mark.parametrize("sq, skv", [(256, 256), (200, 333), (64, 1024),
+                                     (1, 1000), (5, 300)])  # a query or a few: decode-like
 def test_gqa_prefill_kernel(causal, sq, skv):
     B, H, Hkv, D = 2, 8, 2, 128
     dtype = torch.bfloat16
