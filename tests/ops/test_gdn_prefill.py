@@ -77,6 +77,8 @@ def _slow_inputs(B, T, H, seed):
         pytest.param(1, 200, 2, True, marks=pytest.mark.full),  # ragged last chunk
         pytest.param(2, 1000, 3, True, marks=pytest.mark.full),
         pytest.param(1, 37, 1, True, marks=pytest.mark.full),   # shorter than a chunk
+        pytest.param(1, 1, 2, True, marks=pytest.mark.full),    # a single token
+        pytest.param(2, 65, 3, True, marks=pytest.mark.full),   # a chunk and one token
         pytest.param(1, 130, 2, True, marks=pytest.mark.full),   # 3 chunks, ragged
         pytest.param(2, 320, 1, False, marks=pytest.mark.full),  # 5 chunks
         pytest.param(1, 128, 5, True, marks=pytest.mark.full),   # 2 chunks, 5 heads
